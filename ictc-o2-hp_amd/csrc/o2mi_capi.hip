@@ -1,0 +1,425 @@
+// C ABI of the O(2) tensor-product library: plans, geometry, workspace and
+// the fixed-order weight-adjoint reduction.  See include/ictc_o2_hp_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "ictc_o2_hp_amd.h"
+#include "o2mi_tp_launch.hpp"
+
+// Defined by the generated registry (one entry per compiled plan).
+const o2mi::TPKernelSet* o2mi_find_tp_set(int m_max, int full, int normalization);
+
+struct o2mi_tp_plan {
+  const o2mi::TPKernelSet* set;
+  int channels;
+  int m_max;
+  int full;
+  int normalization;
+  int layout;
+  int64_t width;
+  int64_t weight_numel;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& message) {
+  g_last_error = message;
+  return status;
+}
+
+int fail_hip(hipError_t err, const char* where) {
+  g_last_error = std::string(where) + ": " + hipGetErrorString(err);
+  return O2MI_ERR_HIP;
+}
+
+constexpr int kReduceCols = 64;      // columns per reduction block (one per lane)
+constexpr int kReduceSplitRows = 64;  // rows per reduction block in the first pass
+
+// out[s * ncols + col] = sum of in[r * ncols + col] over the rows of split s.
+// Each of the 4 waves sums an interleaved quarter of the rows in order, then
+// the quarters are combined as (q0 + q1) + (q2 + q3): a fixed order.
+__global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ in,
+                                                         int64_t nrows, int64_t ncols,
+                                                         int64_t rows_per_split,
+                                                         float* __restrict__ out) {
+  __shared__ float quarter[4][kReduceCols];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * kReduceCols + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_split;
+  const int64_t r1 = min(nrows, r0 + rows_per_split);
+  float s = 0.f;
+  if (col < ncols) {
+    for (int64_t r = r0 + wave; r < r1; r += 4) s += in[r * ncols + col];
+  }
+  quarter[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && col < ncols) {
+    out[(int64_t)blockIdx.y * ncols + col] =
+        (quarter[0][lane] + quarter[1][lane]) + (quarter[2][lane] + quarter[3][lane]);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ out, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+
+struct DeviceInfo {
+  int cus = 0;
+};
+
+int device_cus() {
+  static std::mutex mu;
+  static DeviceInfo info[64];
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  DeviceInfo& d = info[device & 63];
+  if (d.cus == 0) {
+    hipDeviceProp_t prop;
+    d.cus = hipGetDeviceProperties(&prop, device) == hipSuccess ? prop.multiProcessorCount : 256;
+    if (d.cus <= 0) d.cus = 256;
+  }
+  return d.cus;
+}
+
+int pick_variant(const o2mi_tp_plan* p, std::initializer_list<const void*> ptrs) {
+  if (p->layout != O2MI_LAYOUT_CHANNEL_MAJOR) return o2mi::kVariantComponentMajor;
+  // float2 accesses need every frequency element pair 8-byte aligned.
+  const bool even_rows = p->full || (p->channels % 2 == 0);
+  bool aligned = even_rows;
+  for (const void* q : ptrs) {
+    if (q && (reinterpret_cast<uintptr_t>(q) & 7u)) aligned = false;
+  }
+  return aligned ? o2mi::kVariantChannelMajorVec2 : o2mi::kVariantChannelMajor;
+}
+
+// Rows and lanes per block, rows per block, and the grid for `n_rows` rows
+// when at most `target_blocks` blocks should be resident.
+o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_blocks, int* grid) {
+  o2mi::TPGeom g{};
+  g.n_rows = n_rows;
+  g.channels = p->channels;
+  g.width = (int)p->width;
+  g.weight_numel = (int)p->weight_numel;
+  g.lanes = p->full ? 2 * p->channels : p->channels;
+  if (g.lanes <= o2mi::kBlock) {
+    g.tile_lanes = g.lanes;
+    g.rows_per_iter = o2mi::kBlock / g.lanes;
+    g.tiles = 1;
+  } else {
+    g.tile_lanes = o2mi::kBlock;
+    g.rows_per_iter = 1;
+    g.tiles = (g.lanes + o2mi::kBlock - 1) / o2mi::kBlock;
+  }
+  const int64_t r = g.rows_per_iter;
+  const int64_t iterations = std::max<int64_t>(1, (n_rows + r - 1) / r);
+  const int64_t max_groups = std::max<int64_t>(1, target_blocks / g.tiles);
+  const int64_t groups = std::min(max_groups, iterations);
+  const int64_t iters_per_group = (iterations + groups - 1) / groups;
+  g.rows_per_group = iters_per_group * r;
+  const int64_t used_groups = (iterations + iters_per_group - 1) / iters_per_group;
+  *grid = (int)(used_groups * g.tiles);
+  return g;
+}
+
+struct BackwardShape {
+  o2mi::TPGeom geom;
+  int grid;
+  int variant;
+  int64_t partial_rows;
+  int64_t splits;  // first-pass reduction splits (1: a single pass)
+  size_t bytes;
+};
+
+BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant) {
+  BackwardShape s{};
+  s.variant = variant;
+  const int64_t target = (int64_t)p->set->blocks_per_cu(variant, true) * device_cus();
+  s.geom = geometry(p, n_rows, target, &s.grid);
+  s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
+  s.splits = s.partial_rows <= kReduceSplitRows
+                 ? 1
+                 : std::min<int64_t>(64, (s.partial_rows + kReduceSplitRows - 1) / kReduceSplitRows);
+  const int64_t floats = (s.partial_rows + (s.splits > 1 ? s.splits : 0)) * p->weight_numel;
+  s.bytes = n_rows > 0 ? (size_t)floats * sizeof(float) : 0;
+  return s;
+}
+
+hipError_t fill(float* out, int64_t n, float v, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, out, n,
+                     v);
+  return hipGetLastError();
+}
+
+hipError_t column_sum(const float* in, int64_t nrows, int64_t ncols, int64_t splits, float* out,
+                      hipStream_t stream) {
+  const int64_t per_split = (nrows + splits - 1) / splits;
+  dim3 grid((unsigned)((ncols + kReduceCols - 1) / kReduceCols), (unsigned)splits);
+  hipLaunchKernelGGL(column_sum_kernel, grid, dim3(256), 0, stream, in, nrows, ncols, per_split,
+                     out);
+  return hipGetLastError();
+}
+
+// Optional kernel timing: while enabled, every forward/backward call records
+// a HIP event pair around its main kernel on the call's stream.  Calls may
+// come from any thread (the autograd engine runs backward on its own).
+struct TimedLaunch {
+  int kind;  // 0 forward, 1 backward
+  hipEvent_t start, stop;
+};
+
+std::mutex g_timing_mu;
+bool g_timing = false;
+std::vector<TimedLaunch> g_timed;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Returns the start event to record (or nullptr when timing is off).
+bool timing_begin(hipStream_t s, TimedLaunch* launch, int kind) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  if (!g_timing) return false;
+  launch->kind = kind;
+  launch->start = take_event();
+  launch->stop = take_event();
+  if (!launch->start || !launch->stop) return false;
+  return hipEventRecord(launch->start, s) == hipSuccess;
+}
+
+void timing_end(hipStream_t s, TimedLaunch* launch) {
+  if (hipEventRecord(launch->stop, s) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timed.push_back(*launch);
+}
+
+}  // namespace
+
+extern "C" {
+
+int o2mi_kernel_timing(int enable) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timing = enable != 0;
+  return O2MI_OK;
+}
+
+int o2mi_kernel_timing_read(double* forward_ms, int* forward_count, double* backward_ms,
+                            int* backward_count) {
+  std::vector<TimedLaunch> done;
+  {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    done.swap(g_timed);
+  }
+  double totals[2] = {0.0, 0.0};
+  int counts[2] = {0, 0};
+  int status = O2MI_OK;
+  for (const TimedLaunch& t : done) {
+    float ms = 0.f;
+    if (hipEventSynchronize(t.stop) == hipSuccess &&
+        hipEventElapsedTime(&ms, t.start, t.stop) == hipSuccess) {
+      totals[t.kind] += ms;
+      counts[t.kind] += 1;
+    } else {
+      status = fail(O2MI_ERR_HIP, "kernel timing: event query failed");
+    }
+  }
+  {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    for (const TimedLaunch& t : done) {
+      g_event_pool.push_back(t.start);
+      g_event_pool.push_back(t.stop);
+    }
+  }
+  if (forward_ms) *forward_ms = totals[0];
+  if (forward_count) *forward_count = counts[0];
+  if (backward_ms) *backward_ms = totals[1];
+  if (backward_count) *backward_count = counts[1];
+  return status;
+}
+
+const char* o2mi_last_error(void) { return g_last_error.c_str(); }
+
+const char* o2mi_version(void) { return "ictc_o2_hp_amd 0.1.0 (gfx950)"; }
+
+int o2mi_tp_plan_create(int channels, int m_max, int parity, int normalization, int layout,
+                        o2mi_tp_plan** plan) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan output pointer is NULL");
+  *plan = nullptr;
+  if (channels < 1) return fail(O2MI_ERR_INVALID_ARGUMENT, "channels must be positive");
+  if (m_max < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "m_max must be non-negative");
+  if (parity != O2MI_CANONICAL && parity != O2MI_FULL)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "parity must be canonical (0) or full (1)");
+  if (normalization != O2MI_COMPONENT && normalization != O2MI_NORM)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "normalization must be component (0) or norm (1)");
+  const bool full = parity == O2MI_FULL;
+  const bool layout_ok = layout == O2MI_LAYOUT_CHANNEL_MAJOR ||
+                         (layout == O2MI_LAYOUT_COMPONENT_MAJOR && !full) ||
+                         (layout == O2MI_LAYOUT_COPY_COMPONENT_MAJOR && full);
+  if (!layout_ok) return fail(O2MI_ERR_INVALID_ARGUMENT, "layout does not match the parity");
+  const o2mi::TPKernelSet* set = o2mi_find_tp_set(m_max, full ? 1 : 0, normalization);
+  if (!set) return fail(O2MI_ERR_UNSUPPORTED, "no kernels compiled for this m_max/parity/normalization");
+  // Row width and packed weight count in units of C.
+  int width_units = 0;
+  for (int k = 0; k < set->table.n_keys; ++k) {
+    const o2mi::KeySpec& ks = set->table.keys[k];
+    width_units = std::max(width_units, ks.off + (ks.dim == 1 ? 1 : (full ? 4 : 2)));
+  }
+  o2mi_tp_plan* p = new (std::nothrow) o2mi_tp_plan;
+  if (!p) return fail(O2MI_ERR_INVALID_ARGUMENT, "out of host memory");
+  p->set = set;
+  p->channels = channels;
+  p->m_max = m_max;
+  p->full = full ? 1 : 0;
+  p->normalization = normalization;
+  p->layout = layout;
+  p->width = (int64_t)width_units * channels;
+  p->weight_numel = (int64_t)set->table.n_units * channels;
+  if (p->width * 8 >= (int64_t)INT32_MAX || p->weight_numel >= (int64_t)INT32_MAX / 4096) {
+    delete p;
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "channels too large");
+  }
+  *plan = p;
+  return O2MI_OK;
+}
+
+int o2mi_tp_plan_destroy(o2mi_tp_plan* plan) {
+  delete plan;
+  return O2MI_OK;
+}
+
+int64_t o2mi_tp_width(const o2mi_tp_plan* plan) { return plan ? plan->width : -1; }
+
+int64_t o2mi_tp_weight_numel(const o2mi_tp_plan* plan) { return plan ? plan->weight_numel : -1; }
+
+int o2mi_tp_table(int m_max, int parity, int normalization, int* n_paths, int* n_terms,
+                  int32_t* paths, float* magnitudes, int32_t* terms) {
+  const o2mi::TPKernelSet* set = o2mi_find_tp_set(m_max, parity == O2MI_FULL ? 1 : 0, normalization);
+  if (!set) return fail(O2MI_ERR_UNSUPPORTED, "no kernels compiled for this m_max/parity/normalization");
+  const o2mi::TPTableView& t = set->table;
+  if (n_paths) *n_paths = t.n_paths;
+  if (n_terms) *n_terms = t.n_terms;
+  for (int p = 0; p < t.n_paths; ++p) {
+    const o2mi::PathSpec& ps = t.paths[p];
+    if (paths) {
+      int32_t* row = paths + 7 * p;
+      row[0] = ps.k1;
+      row[1] = ps.k2;
+      row[2] = ps.k3;
+      row[3] = ps.wunits;
+      row[4] = ps.t0;
+      row[5] = ps.nt;
+      row[6] = t.keys[ps.k3].dim;
+    }
+    if (magnitudes) magnitudes[p] = ps.mag;
+  }
+  if (terms) {
+    for (int n = 0; n < t.n_terms; ++n) {
+      terms[4 * n + 0] = t.terms[n].i;
+      terms[4 * n + 1] = t.terms[n].j;
+      terms[4 * n + 2] = t.terms[n].k;
+      terms[4 * n + 3] = t.terms[n].sign;
+    }
+  }
+  return O2MI_OK;
+}
+
+int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y, const float* w,
+                        float* out, int64_t n_rows, void* stream) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
+  if (n_rows == 0) return O2MI_OK;
+  if (!x || !y || !w || !out) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (n_rows > (int64_t)INT32_MAX * 64)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int variant = pick_variant(plan, {x, y, out});
+  const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
+  int grid = 0;
+  const o2mi::TPGeom g = geometry(plan, n_rows, target, &grid);
+  TimedLaunch timed;
+  const bool timing = timing_begin(s, &timed, 0);
+  const hipError_t err = plan->set->forward(variant, x, y, w, out, g, grid, s);
+  if (timing) timing_end(s, &timed);
+  if (err != hipSuccess) return fail_hip(err, "tp forward launch");
+  return O2MI_OK;
+}
+
+size_t o2mi_tp_backward_workspace_bytes(const o2mi_tp_plan* plan, int64_t n_rows) {
+  if (!plan || n_rows <= 0) return 0;
+  // The variant only changes the occupancy query; size for the largest.
+  size_t bytes = 0;
+  for (int v = 0; v < o2mi::kNumVariants; ++v) {
+    if ((plan->layout == O2MI_LAYOUT_CHANNEL_MAJOR) != (v != o2mi::kVariantComponentMajor)) continue;
+    bytes = std::max(bytes, backward_shape(plan, n_rows, v).bytes);
+  }
+  return bytes;
+}
+
+int o2mi_tp_backward_f32(const o2mi_tp_plan* plan, const float* x, const float* y, const float* w,
+                         const float* g, float* dx, float* dy, float* dw, void* workspace,
+                         size_t workspace_bytes, int64_t n_rows, int needed, void* stream) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
+  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
+  if ((needed & 4) && !dw) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL dw for a requested gradient");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_rows == 0 || needed == 0) {
+    // Empty inputs: dx and dy are empty (their pointers may be NULL), dw = 0.
+    if (needed & 4) {
+      const hipError_t err = fill(dw, plan->weight_numel, 0.f, s);
+      if (err != hipSuccess) return fail_hip(err, "dw fill");
+    }
+    return O2MI_OK;
+  }
+  if (!x || !y || !w || !g) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
+  if (((needed & 1) && !dx) || ((needed & 2) && !dy))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
+  if (n_rows > (int64_t)INT32_MAX * 64)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  const int variant = pick_variant(plan, {x, y, g, (needed & 1) ? dx : nullptr,
+                                          (needed & 2) ? dy : nullptr});
+  const BackwardShape shape = backward_shape(plan, n_rows, variant);
+  if ((needed & 4) && (!workspace || workspace_bytes < shape.bytes))
+    return fail(O2MI_ERR_WORKSPACE, "workspace smaller than o2mi_tp_backward_workspace_bytes");
+  float* partial = static_cast<float*>(workspace);
+  TimedLaunch timed;
+  const bool timing = timing_begin(s, &timed, 1);
+  hipError_t err = plan->set->backward(variant, x, y, w, g, dx, dy, partial, shape.geom,
+                                       shape.grid, needed, s);
+  if (timing) timing_end(s, &timed);
+  if (err != hipSuccess) return fail_hip(err, "tp backward launch");
+  if (needed & 4) {
+    const int64_t pw = plan->weight_numel;
+    if (shape.splits == 1) {
+      err = column_sum(partial, shape.partial_rows, pw, 1, dw, s);
+    } else {
+      float* second = partial + shape.partial_rows * pw;
+      err = column_sum(partial, shape.partial_rows, pw, shape.splits, second, s);
+      if (err == hipSuccess) err = column_sum(second, shape.splits, pw, 1, dw, s);
+    }
+    if (err != hipSuccess) return fail_hip(err, "dw reduction launch");
+  }
+  return O2MI_OK;
+}
+
+}  // extern "C"

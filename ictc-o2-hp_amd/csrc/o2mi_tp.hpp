@@ -1,0 +1,476 @@
+// O(2) tensor-product kernels for gfx950 (CDNA4): forward and fused VJP.
+//
+// One plan P (generated per m_max / parity / normalization) supplies the
+// key table, the path table and each path's sparse coupling terms as
+// constexpr data; every loop over keys, paths and terms below is unrolled at
+// compile time, so coefficients become sign modifiers or folded constants
+// and the per-lane state lives in registers.
+//
+// Work mapping.  A flat row holds, per key, C scalars (0e, 0o) or 2C x 2
+// floats (frequency blocks of full parity: [copy, channel, component]).  A
+// "lane" is one (channel c, copy q) of a row: 2C lanes per row for full
+// parity, C for canonical.  Neighbouring hardware lanes 2c, 2c+1 hold the two
+// copies of channel c, so
+//   * frequency outputs of copy q read copy q of frequency inputs and the
+//     channel-c scalars (routing o mod mul of native_o2.py:128-129),
+//   * scalar outputs read copy 0 only: they are produced by the q = 0 lane,
+//   * the scalar input adjoints, which collect both copies, finish with one
+//     DPP swap between the two lanes of a pair.
+// Copy-1 values are turned into the canonical basis on load, (v0, v1) ->
+// (-v1, v0), and back on store (fast_o2.py:61-73, triton_o2.py:133-164).
+//
+// Memory access.  Rows are read and written with buffer instructions: a
+// per-iteration descriptor (SGPRs) whose base is the iteration's first row and
+// whose size covers exactly the valid rows, a loop-invariant per-lane byte
+// offset (VGPR) and a per-key uniform offset (SGPR).  Rows past the end and
+// idle lanes fall outside the descriptor, so their loads return 0 and their
+// stores are dropped by the hardware: no branches, no masks.
+//
+// Both kernels are persistent: block b owns a fixed, contiguous range of
+// rows and a fixed set of lanes, so the backward keeps one weight-adjoint
+// accumulator per path and lane in registers across all its rows and writes
+// one partial row at the end; a fixed-order column sum finishes dw.  There
+// are no atomics and the result is bitwise reproducible.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace o2mi {
+
+struct KeySpec {
+  int off;  // offset in the row, in units of C
+  int dim;  // 1 for scalars, 2 for frequency keys
+};
+
+struct PathSpec {
+  int k1, k2, k3;  // key indices
+  int wunits;      // first packed weight, in units of C
+  int t0, nt;      // terms[t0 .. t0 + nt)
+  float mag;       // common |coefficient| of the terms
+};
+
+struct TermSpec {
+  int i, j, k;  // first, second and output component
+  int sign;     // +1 or -1
+};
+
+constexpr int kBlock = 256;
+// Byte offset given to lanes with nothing to load or store: beyond any
+// descriptor size used here (< 2^31), with room to add key offsets.
+constexpr uint32_t kIdle = 0x80000000u;
+// Word 3 of a raw gfx9 buffer descriptor (32-bit data format).
+constexpr int kRsrcFlags = 0x00020000;
+
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+// Launch geometry, computed on the host (o2mi_capi.hip).
+struct TPGeom {
+  int64_t n_rows;
+  int64_t rows_per_group;  // rows owned by one block (multiple of rows_per_iter)
+  int channels;            // C
+  int width;               // W, floats per row
+  int lanes;               // lanes per row: 2C (full) or C (canonical)
+  int tile_lanes;          // lanes of one row handled by a block: min(lanes, 256)
+  int rows_per_iter;       // rows a block advances per iteration
+  int tiles;               // blocks sharing one row range: ceil(lanes / 256)
+  int weight_numel;        // P_w
+};
+
+struct Lane {
+  int c;     // channel (clamped to 0 on idle lanes)
+  int q;     // copy (always 0 for canonical parity)
+  int cloc;  // channel index inside the block's tile
+  int slot;  // row slot inside one iteration
+  bool active;
+};
+
+template <bool kFull>
+__device__ __forceinline__ Lane make_lane(const TPGeom& g, int tile) {
+  Lane l;
+  const int t = threadIdx.x;
+  int jloc;
+  if (g.tiles == 1) {
+    l.slot = t / g.tile_lanes;
+    jloc = t - l.slot * g.tile_lanes;
+  } else {
+    l.slot = 0;
+    jloc = t;
+  }
+  const int j = tile * kBlock + jloc;
+  l.active = l.slot < g.rows_per_iter && j < g.lanes;
+  const int jj = l.active ? j : 0;
+  l.c = kFull ? (jj >> 1) : jj;
+  l.q = kFull ? (jj & 1) : 0;
+  l.cloc = kFull ? (jloc >> 1) : jloc;
+  return l;
+}
+
+// Per-lane byte offsets inside one iteration's rows.
+struct LaneOffsets {
+  uint32_t scalar;       // scalar keys
+  uint32_t freq;         // frequency keys, component 0
+  uint32_t scalar_own;   // scalar keys of the copy-0 lane only (idle on copy 1)
+};
+
+template <bool kFull, int kLayout>
+__device__ __forceinline__ LaneOffsets lane_offsets(const TPGeom& g, const Lane& l) {
+  LaneOffsets o;
+  const int row = l.slot * g.width;
+  const int f = (kFull ? l.q * 2 * g.channels : 0) + (kLayout == 0 ? 2 * l.c : l.c);
+  o.scalar = l.active ? (uint32_t)(row + l.c) * 4u : kIdle;
+  o.freq = l.active ? (uint32_t)(row + f) * 4u : kIdle;
+  o.scalar_own = (l.active && l.q == 0) ? o.scalar : kIdle;
+  return o;
+}
+
+// Descriptor over rows [row0, row0 + rows) of a [*, width] f32 tensor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int64_t row0,
+                                                            int width, int rows) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base) + row0 * width, 0,
+                                           rows * width * 4, kRsrcFlags);
+}
+
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, 0));
+}
+
+using f32x2 = float __attribute__((ext_vector_type(2)));
+using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+
+// Whole-vector bit casts only: hipcc 7.2 miscompiles __builtin_bit_cast of a
+// single vector element (both elements read as element 0).
+__device__ __forceinline__ void bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff,
+                                       float& a, float& b) {
+  const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, 0));
+  a = v.x;
+  b = v.y;
+}
+
+__device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff,
+                                       int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, soff, 0);
+}
+
+__device__ __forceinline__ void bstore2(__amdgpu_buffer_rsrc_t r, float a, float b,
+                                        uint32_t voff, int soff) {
+  f32x2 v;
+  v.x = a;
+  v.y = b;
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)voff, soff, 0);
+}
+
+// Exchange a value between the two lanes of a copy pair (quad_perm 1,0,3,2).
+__device__ __forceinline__ float pair_swap(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+
+template <class P, int kLayout, bool kVec2, int K>
+__device__ __forceinline__ void load_key(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
+                                         uint32_t voff, float& v0, float& v1) {
+  constexpr KeySpec ks = P::keys[K];
+  const int soff = ks.off * C * 4;
+  if constexpr (ks.dim == 1) {
+    v0 = bload(r, voff, soff);
+    v1 = 0.f;
+  } else {
+    float a0, a1;
+    if constexpr (kLayout == 0 && kVec2) {
+      bload2(r, voff, soff, a0, a1);
+    } else if constexpr (kLayout == 0) {
+      a0 = bload(r, voff, soff);
+      a1 = bload(r, voff + 4u, soff);
+    } else {
+      a0 = bload(r, voff, soff);
+      a1 = bload(r, voff, soff + C * 4);
+    }
+    if constexpr (P::kFull) {
+      const bool odd = l.q != 0;
+      v0 = odd ? -a1 : a0;
+      v1 = odd ? a0 : a1;
+    } else {
+      v0 = a0;
+      v1 = a1;
+    }
+  }
+}
+
+template <class P, int kLayout, bool kVec2, int K>
+__device__ __forceinline__ void store_key(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
+                                          uint32_t voff, float v0, float v1) {
+  constexpr KeySpec ks = P::keys[K];
+  const int soff = ks.off * C * 4;
+  if constexpr (ks.dim == 1) {
+    bstore(r, v0, voff, soff);
+  } else {
+    float s0 = v0, s1 = v1;
+    if constexpr (P::kFull) {
+      const bool odd = l.q != 0;
+      s0 = odd ? v1 : v0;
+      s1 = odd ? -v0 : v1;
+    }
+    if constexpr (kLayout == 0 && kVec2) {
+      bstore2(r, s0, s1, voff, soff);
+    } else if constexpr (kLayout == 0) {
+      bstore(r, s0, voff, soff);
+      bstore(r, s1, voff + 4u, soff);
+    } else {
+      bstore(r, s0, voff, soff);
+      bstore(r, s1, voff, soff + C * 4);
+    }
+  }
+}
+
+// Loads every key of one row set: x and y, and optionally the cotangent.
+template <class P, int kLayout, bool kVec2>
+__device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
+                                         const LaneOffsets& o, bool copy0_scalars,
+                                         float (&V)[P::kKeys][2]) {
+  static_for<P::kKeys>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const uint32_t voff =
+        P::keys[k].dim == 1 ? (copy0_scalars ? o.scalar_own : o.scalar) : o.freq;
+    load_key<P, kLayout, kVec2, k>(r, C, l, voff, V[k][0], V[k][1]);
+  });
+}
+
+template <class P, int kLayout, bool kVec2>
+__device__ __forceinline__ void store_row(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
+                                          const LaneOffsets& o, const float (&V)[P::kKeys][2]) {
+  static_for<P::kKeys>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    // Scalar keys are written by the copy-0 lane only.
+    const uint32_t voff = P::keys[k].dim == 1 ? o.scalar_own : o.freq;
+    store_key<P, kLayout, kVec2, k>(r, C, l, voff, V[k][0], V[k][1]);
+  });
+}
+
+template <class P, int kPath>
+__device__ __forceinline__ void path_value(const float (&X)[P::kKeys][2],
+                                           const float (&Y)[P::kKeys][2], float& f0, float& f1) {
+  constexpr PathSpec ps = P::paths[kPath];
+  f0 = 0.f;
+  f1 = 0.f;
+  static_for<ps.nt>([&](auto tc) {
+    constexpr TermSpec ts = P::terms[ps.t0 + decltype(tc)::value];
+    const float a = ts.sign > 0 ? X[ps.k1][ts.i] : -X[ps.k1][ts.i];
+    if constexpr (ts.k == 0) {
+      f0 = fmaf(a, Y[ps.k2][ts.j], f0);
+    } else {
+      f1 = fmaf(a, Y[ps.k2][ts.j], f1);
+    }
+  });
+}
+
+template <class P>
+constexpr bool out_is_freq(int p) {
+  return P::keys[P::paths[p].k3].dim == 2;
+}
+
+// Rows of iteration `it` that exist: the descriptor covers exactly these.
+__device__ __forceinline__ int iteration_rows(const TPGeom& g, int64_t r0, int64_t r1, int it) {
+  const int64_t left = r1 - (r0 + (int64_t)it * g.rows_per_iter);
+  return left <= 0 ? 0 : (left < g.rows_per_iter ? (int)left : g.rows_per_iter);
+}
+
+// ---------------------------------------------------------------------------
+// Forward: out = sum over paths of w * CG(x, y)  (native_o2.py:209-221).
+// Weights (times the path magnitude) are held in registers for all rows.
+template <class P, int kLayout, bool kVec2>
+__global__ __launch_bounds__(kBlock) void tp_forward_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ y,
+                                                           const float* __restrict__ w,
+                                                           float* __restrict__ out, TPGeom g) {
+  const int tile = blockIdx.x % g.tiles;
+  const int64_t group = blockIdx.x / g.tiles;
+  const Lane l = make_lane<P::kFull>(g, tile);
+  const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
+  const int C = g.channels;
+
+  float wr[P::kPaths];
+  static_for<P::kPaths>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr PathSpec ps = P::paths[p];
+    const int oc = ((out_is_freq<P>(p) && P::kFull) ? l.q * C : 0) + l.c;
+    wr[p] = l.active ? w[ps.wunits * C + oc] * ps.mag : 0.f;
+  });
+
+  const int64_t r0 = group * g.rows_per_group;
+  const int64_t r1 = min(g.n_rows, r0 + g.rows_per_group);
+  const int iters = r1 > r0 ? (int)((r1 - r0 + g.rows_per_iter - 1) / g.rows_per_iter) : 0;
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row0 = r0 + (int64_t)it * g.rows_per_iter;
+    const int rows = iteration_rows(g, r0, r1, it);
+    const auto rx = rows_rsrc(x, row0, g.width, rows);
+    const auto ry = rows_rsrc(y, row0, g.width, rows);
+    const auto ro = rows_rsrc(out, row0, g.width, rows);
+    float X[P::kKeys][2], Y[P::kKeys][2];
+    load_row<P, kLayout, kVec2>(rx, C, l, o, false, X);
+    load_row<P, kLayout, kVec2>(ry, C, l, o, false, Y);
+    float A[P::kKeys][2];
+    static_for<P::kKeys>([&](auto kc) {
+      A[decltype(kc)::value][0] = 0.f;
+      A[decltype(kc)::value][1] = 0.f;
+    });
+    static_for<P::kPaths>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr PathSpec ps = P::paths[p];
+      float f0, f1;
+      path_value<P, p>(X, Y, f0, f1);
+      A[ps.k3][0] = fmaf(wr[p], f0, A[ps.k3][0]);
+      if constexpr (out_is_freq<P>(p)) A[ps.k3][1] = fmaf(wr[p], f1, A[ps.k3][1]);
+    });
+    store_row<P, kLayout, kVec2>(ro, C, l, o, A);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused VJP: dx, dy and the weight adjoint in one pass over x, y, g.
+//   dx[k1][i] += w * coef * g[k3][k] * y[k2][j]       (triton_o2.py:452-501)
+//   dy[k2][j] += w * coef * g[k3][k] * x[k1][i]
+//   dw[p, o]  += coef * x[k1][i] * y[k2][j] * g[k3][k] (triton_o2.py:571-607)
+// Weights times magnitudes are staged in LDS as [weight unit][kStride] with
+// kStride = 128 (full: channels per 256-lane tile) or 256 (canonical).  The
+// next iteration's rows are loaded while the current one is computed.
+template <class P>
+constexpr int lds_stride() {
+  return P::kFull ? kBlock / 2 : kBlock;
+}
+
+template <class P>
+constexpr size_t backward_lds_bytes() {
+  return sizeof(float) * (size_t)P::kUnits * (size_t)lds_stride<P>();
+}
+
+template <class P, int kLayout, bool kVec2>
+__global__ __launch_bounds__(kBlock, 2) void tp_backward_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
+    const float* __restrict__ gout, float* __restrict__ dx, float* __restrict__ dy,
+    float* __restrict__ partial, TPGeom g, int needed) {
+  constexpr int kStride = lds_stride<P>();
+  extern __shared__ float lds_w[];
+  const int tile = blockIdx.x % g.tiles;
+  const int64_t group = blockIdx.x / g.tiles;
+  const Lane l = make_lane<P::kFull>(g, tile);
+  const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
+  const int C = g.channels;
+
+  // Stage this tile's weights: unit u, column col <-> w[u * C + c0 + col].
+  {
+    const int c0 = tile * kStride;
+    const int col = threadIdx.x;
+    static_for<P::kUnits>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      if (col < kStride) {
+        const int c = c0 + col;
+        lds_w[u * kStride + col] = c < C ? w[u * C + c] * P::unit_mag[u] : 0.f;
+      }
+    });
+  }
+  __syncthreads();
+
+  // Per-lane LDS columns of frequency-output and scalar-output weights.
+  int col_freq = (P::kFull ? l.q * kStride : 0) + l.cloc;
+  int col_scalar = l.cloc;
+
+  float dwacc[P::kPaths];
+  static_for<P::kPaths>([&](auto pc) { dwacc[decltype(pc)::value] = 0.f; });
+
+  const int64_t r0 = group * g.rows_per_group;
+  const int64_t r1 = min(g.n_rows, r0 + g.rows_per_group);
+  const int iters = r1 > r0 ? (int)((r1 - r0 + g.rows_per_iter - 1) / g.rows_per_iter) : 0;
+  // Stores of roles that were not requested go to idle offsets (dropped).
+  LaneOffsets ox = o, oy = o;
+  if (!(needed & 1)) ox.scalar_own = ox.freq = kIdle;
+  if (!(needed & 2)) oy.scalar_own = oy.freq = kIdle;
+
+  float X[P::kKeys][2], Y[P::kKeys][2], G[P::kKeys][2];
+  {
+    const int rows = iteration_rows(g, r0, r1, 0);
+    load_row<P, kLayout, kVec2>(rows_rsrc(x, r0, g.width, rows), C, l, o, false, X);
+    load_row<P, kLayout, kVec2>(rows_rsrc(y, r0, g.width, rows), C, l, o, false, Y);
+    // Scalar outputs belong to the copy-0 lane; the copy-1 lane reads a zero
+    // cotangent there, which removes its (wrong-copy) contributions.
+    load_row<P, kLayout, kVec2>(rows_rsrc(gout, r0, g.width, rows), C, l, o, true, G);
+  }
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row0 = r0 + (int64_t)it * g.rows_per_iter;
+    const int rows = iteration_rows(g, r0, r1, it);
+    const int64_t row_next = row0 + g.rows_per_iter;
+    const int rows_next = iteration_rows(g, r0, r1, it + 1);
+    float Xn[P::kKeys][2], Yn[P::kKeys][2], Gn[P::kKeys][2];
+    load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
+    load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
+    load_row<P, kLayout, kVec2>(rows_rsrc(gout, row_next, g.width, rows_next), C, l, o, true, Gn);
+
+    float DX[P::kKeys][2], DY[P::kKeys][2];
+    static_for<P::kKeys>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      DX[k][0] = DX[k][1] = DY[k][0] = DY[k][1] = 0.f;
+    });
+    // Re-read the weights from LDS every iteration: hoisting the 85-odd
+    // loop-invariant reads out of the loop would cost as many registers.
+    asm volatile("" : "+v"(col_freq), "+v"(col_scalar));
+    static_for<P::kPaths>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr PathSpec ps = P::paths[p];
+      constexpr bool freq3 = out_is_freq<P>(p);
+      const float wv = lds_w[(freq3 ? col_freq : col_scalar) + ps.wunits * kStride];
+      float f0, f1;
+      path_value<P, p>(X, Y, f0, f1);
+      dwacc[p] = fmaf(G[ps.k3][0], f0, dwacc[p]);
+      if constexpr (freq3) dwacc[p] = fmaf(G[ps.k3][1], f1, dwacc[p]);
+      const float h[2] = {wv * G[ps.k3][0], freq3 ? wv * G[ps.k3][1] : 0.f};
+      static_for<ps.nt>([&](auto tc) {
+        constexpr TermSpec ts = P::terms[ps.t0 + decltype(tc)::value];
+        const float hk = ts.sign > 0 ? h[ts.k] : -h[ts.k];
+        DX[ps.k1][ts.i] = fmaf(hk, Y[ps.k2][ts.j], DX[ps.k1][ts.i]);
+        DY[ps.k2][ts.j] = fmaf(hk, X[ps.k1][ts.i], DY[ps.k2][ts.j]);
+      });
+    });
+    if constexpr (P::kFull) {
+      static_for<P::kKeys>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (P::keys[k].dim == 1) {
+          DX[k][0] += pair_swap(DX[k][0]);
+          DY[k][0] += pair_swap(DY[k][0]);
+        }
+      });
+    }
+    store_row<P, kLayout, kVec2>(rows_rsrc(dx, row0, g.width, rows), C, l, ox, DX);
+    store_row<P, kLayout, kVec2>(rows_rsrc(dy, row0, g.width, rows), C, l, oy, DY);
+
+    static_for<P::kKeys>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      X[k][0] = Xn[k][0];
+      X[k][1] = Xn[k][1];
+      Y[k][0] = Yn[k][0];
+      Y[k][1] = Yn[k][1];
+      G[k][0] = Gn[k][0];
+      G[k][1] = Gn[k][1];
+    });
+  }
+
+  if ((needed & 4) && l.active) {
+    float* prow = partial + (group * g.rows_per_iter + l.slot) * (int64_t)g.weight_numel;
+    static_for<P::kPaths>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr PathSpec ps = P::paths[p];
+      if (out_is_freq<P>(p) || l.q == 0) {
+        const int oc = ((out_is_freq<P>(p) && P::kFull) ? l.q * C : 0) + l.c;
+        prow[ps.wunits * C + oc] = dwacc[p] * ps.mag;
+      }
+    });
+  }
+}
+
+}  // namespace o2mi

@@ -1,0 +1,179 @@
+"""torch.library ops over the C ABI: ``o2_forward`` and ``o2_backward``.
+
+Schemas follow the reference's ops (``triton_o2.py:786-794``, ``:878-887``):
+``o2_forward(left, right, weight, path_info, path_coefficients, metadata_id)``
+and ``o2_backward(left, right, weight, grad_output, path_info,
+path_coefficients, metadata_id) -> (grad_left, grad_right, grad_weight)``.
+``metadata_id`` indexes this process's plan registry; ``path_info`` and
+``path_coefficients`` are the reference's int32 [P, 25] / f32 [P, 4] path
+metadata, carried for schema compatibility (the compiled kernels embed the
+same table).  Each op has a fake implementation and autograd, so
+``torch.compile(fullgraph=True)`` traces through it; the backward's own
+derivative (second order) recomputes with the PyTorch algebra, as the
+reference does (``triton_o2.py:1035-1069``).
+
+Outputs and workspaces come from torch's caching allocator; kernels run on
+the current stream.  A CUDA tensor without the built library raises.
+"""
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass, field
+from typing import Dict
+
+import torch
+
+from . import __version__
+from . import _native
+from .plan import TPPlan
+from .torch_algebra import flat_forward
+
+NAMESPACE = "ictc_o2_hp_amd_v" + __version__.replace(".", "_")
+
+
+@dataclass
+class _Registered:
+    plan: TPPlan
+    layout: int
+    native: Dict[int, _native.TPNativePlan] = field(default_factory=dict)
+
+
+_REGISTRY: Dict[int, _Registered] = {}
+_REGISTRY_LOCK = threading.Lock()
+
+
+def register(plan: TPPlan, layout: int) -> int:
+    """Register a module's plan; returns its ``metadata_id``."""
+    with _REGISTRY_LOCK:
+        metadata_id = len(_REGISTRY)
+        _REGISTRY[metadata_id] = _Registered(plan, layout)
+    return metadata_id
+
+
+def registered(metadata_id: int) -> _Registered:
+    return _REGISTRY[metadata_id]
+
+
+def _native_plan(metadata_id: int) -> _native.TPNativePlan:
+    entry = _REGISTRY[metadata_id]
+    native = entry.native.get(0)
+    if native is None:
+        with _REGISTRY_LOCK:
+            native = entry.native.get(0)
+            if native is None:
+                plan = entry.plan
+                native = _native.TPNativePlan(plan.channels, plan.m_max, plan.parity,
+                                              plan.normalization, entry.layout)
+                if native.width != plan.width or native.weight_numel != plan.weight_numel:
+                    raise _native.NativeLibraryError("compiled plan disagrees with the host plan")
+                entry.native[0] = native
+    return native
+
+
+def _check_inputs(*tensors: torch.Tensor) -> None:
+    device = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda" or t.device != device:
+            raise ValueError("o2 ops need CUDA(HIP) tensors on one device")
+        if t.dtype != torch.float32:
+            raise ValueError("o2 ops compute in float32")
+        if not t.is_contiguous():
+            raise ValueError("o2 ops need contiguous tensors")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+@torch.library.custom_op(NAMESPACE + "::o2_forward", mutates_args=())
+def o2_forward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
+               path_info: torch.Tensor, path_coefficients: torch.Tensor,
+               metadata_id: int) -> torch.Tensor:
+    _check_inputs(left, right, weight)
+    native = _native_plan(metadata_id)
+    n_rows, width = left.shape
+    if width != native.width or right.shape != left.shape or weight.numel() != native.weight_numel:
+        raise ValueError("o2_forward: shapes do not match the plan")
+    out = torch.empty_like(left)
+    with torch.cuda.device(left.device):
+        native.forward(left.data_ptr(), right.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                       n_rows, _stream(left.device))
+    return out
+
+
+@o2_forward.register_fake
+def _o2_forward_fake(left, right, weight, path_info, path_coefficients, metadata_id):
+    return torch.empty_like(left)
+
+
+@torch.library.custom_op(NAMESPACE + "::o2_backward", mutates_args=())
+def o2_backward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
+                grad_output: torch.Tensor, path_info: torch.Tensor,
+                path_coefficients: torch.Tensor,
+                metadata_id: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    grad_output = grad_output.contiguous()
+    _check_inputs(left, right, weight, grad_output)
+    native = _native_plan(metadata_id)
+    n_rows, width = left.shape
+    if width != native.width or grad_output.shape != left.shape:
+        raise ValueError("o2_backward: shapes do not match the plan")
+    grad_left = torch.empty_like(left)
+    grad_right = torch.empty_like(right)
+    grad_weight = torch.empty_like(weight)
+    ws_bytes = native.workspace_bytes(n_rows)
+    workspace = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=left.device)
+    with torch.cuda.device(left.device):
+        native.backward(left.data_ptr(), right.data_ptr(), weight.data_ptr(),
+                        grad_output.data_ptr(), grad_left.data_ptr(), grad_right.data_ptr(),
+                        grad_weight.data_ptr(), workspace.data_ptr(), ws_bytes, n_rows, 7,
+                        _stream(left.device))
+    return grad_left, grad_right, grad_weight
+
+
+@o2_backward.register_fake
+def _o2_backward_fake(left, right, weight, grad_output, path_info, path_coefficients,
+                      metadata_id):
+    return torch.empty_like(left), torch.empty_like(right), torch.empty_like(weight)
+
+
+def _forward_setup(ctx, inputs, output):
+    left, right, weight, path_info, path_coefficients, metadata_id = inputs
+    ctx.save_for_backward(left, right, weight, path_info, path_coefficients)
+    ctx.metadata_id = metadata_id
+
+
+def _forward_backward(ctx, grad_output):
+    left, right, weight, path_info, path_coefficients = ctx.saved_tensors
+    grads = o2_backward(left, right, weight, grad_output, path_info, path_coefficients,
+                        ctx.metadata_id)
+    return (*grads, None, None, None)
+
+
+o2_forward.register_autograd(_forward_backward, setup_context=_forward_setup)
+
+
+def _backward_setup(ctx, inputs, output):
+    left, right, weight, grad_output, _info, _coef, metadata_id = inputs
+    ctx.save_for_backward(left, right, weight, grad_output)
+    ctx.metadata_id = metadata_id
+
+
+def _backward_backward(ctx, dd_left, dd_right, dd_weight):
+    """Second order: differentiate the first VJP of the PyTorch algebra."""
+    left, right, weight, grad_output = ctx.saved_tensors
+    selected = [(i, c) for i, c in enumerate((dd_left, dd_right, dd_weight)) if c is not None]
+    if not selected:
+        return (None,) * 7
+    entry = registered(ctx.metadata_id)
+    with torch.enable_grad():
+        inputs = tuple(t.detach().requires_grad_(True)
+                       for t in (left, right, weight, grad_output))
+        value = flat_forward(*inputs[:3], entry.plan, entry.layout)
+        first = torch.autograd.grad(value, inputs[:3], inputs[3], create_graph=True)
+        second = torch.autograd.grad(tuple(first[i] for i, _ in selected), inputs,
+                                     grad_outputs=tuple(c for _, c in selected),
+                                     allow_unused=True)
+    return (*second, None, None, None)
+
+
+o2_backward.register_autograd(_backward_backward, setup_context=_backward_setup)

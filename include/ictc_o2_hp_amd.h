@@ -1,0 +1,105 @@
+/*
+ * ictc_o2_hp_amd.h -- C ABI of the MI355X (gfx950) O(2) tensor-product kernels.
+ *
+ * Plain C: raw device pointers, row counts, a plan handle, a caller-provided
+ * workspace and a hipStream_t (passed as void*).  The library never allocates
+ * device memory and never synchronises the stream; every call is
+ * asynchronous on `stream`.  Every entry point returns O2MI_OK (0) or a
+ * negative status; o2mi_last_error() describes the most recent failure of the
+ * calling thread.
+ *
+ * Each declaration names the reference interface it replaces
+ * (Parity-LRX/ICTC-O2-HP, src/ictc_o2_hp/...).
+ */
+#ifndef ICTC_O2_HP_AMD_H
+#define ICTC_O2_HP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum o2mi_status {
+  O2MI_OK = 0,
+  O2MI_ERR_INVALID_ARGUMENT = -1, /* bad pointer, size, shape or flag */
+  O2MI_ERR_UNSUPPORTED = -2,      /* no kernel compiled for this plan */
+  O2MI_ERR_WORKSPACE = -3,        /* workspace missing or too small */
+  O2MI_ERR_HIP = -4,              /* a HIP runtime call failed */
+};
+
+enum o2mi_parity { O2MI_CANONICAL = 0, O2MI_FULL = 1 };
+enum o2mi_normalization { O2MI_COMPONENT = 0, O2MI_NORM = 1 };
+/* Flat row layouts of triton_o2.py:99-121: 0 = channel-major
+ * [copy, channel, component]; 1 = canonical component-major
+ * [component, channel]; 2 = full component-major [copy, component, channel]. */
+enum o2mi_layout { O2MI_LAYOUT_CHANNEL_MAJOR = 0, O2MI_LAYOUT_COMPONENT_MAJOR = 1,
+                   O2MI_LAYOUT_COPY_COMPONENT_MAJOR = 2 };
+/* Gradient roles of a backward call (bit mask). */
+enum o2mi_needed { O2MI_NEED_X = 1, O2MI_NEED_Y = 2, O2MI_NEED_W = 4 };
+
+typedef struct o2mi_tp_plan o2mi_tp_plan;
+
+/* Status text of the calling thread's last failure ("" if none). */
+const char *o2mi_last_error(void);
+
+/* Library version string. */
+const char *o2mi_version(void);
+
+/* Create an immutable plan for TensorProduct(channels, m_max, parity,
+ * normalization) with flat layout `layout`.  Replaces the per-module
+ * metadata registration of triton_o2.py:1098-1132 (_METADATA / metadata_id)
+ * and the layout override of triton_o2.py:1226-1234.  A plan may be shared
+ * by threads. */
+int o2mi_tp_plan_create(int channels, int m_max, int parity, int normalization,
+                        int layout, o2mi_tp_plan **plan);
+int o2mi_tp_plan_destroy(o2mi_tp_plan *plan);
+
+/* Row width W and packed weight count P_w of the plan
+ * (representation_dimension and weight.numel(), native_o2.py:137-143). */
+int64_t o2mi_tp_width(const o2mi_tp_plan *plan);
+int64_t o2mi_tp_weight_numel(const o2mi_tp_plan *plan);
+
+/* Compiled path table of (m_max, parity, normalization), for verification
+ * against the host-side plan.  With `paths`/`terms` NULL only the counts are
+ * returned.  paths[7*p..] = k1, k2, k3, weight_units, first_term, n_terms,
+ * out_dim; magnitudes[p] = common |coefficient|; terms[4*t..] = i, j, k, sign.
+ * Host-only: needs no GPU. */
+int o2mi_tp_table(int m_max, int parity, int normalization, int *n_paths,
+                  int *n_terms, int32_t *paths, float *magnitudes, int32_t *terms);
+
+/* out[N, W] = TP(x, y; w).  Replaces the o2_forward op
+ * (triton_o2.py:786-875): x, y, out are contiguous f32 [N, W]; w is the packed
+ * f32 weight [P_w].  n_rows may be 0. */
+int o2mi_tp_forward_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
+                        const float *w, float *out, int64_t n_rows, void *stream);
+
+/* Bytes of workspace o2mi_tp_backward_f32 needs for n_rows rows. */
+size_t o2mi_tp_backward_workspace_bytes(const o2mi_tp_plan *plan, int64_t n_rows);
+
+/* (dx, dy, dw) = VJP of the forward at cotangent g.  Replaces the o2_backward
+ * op (triton_o2.py:878-966): the input adjoint of :452-568 and the
+ * deterministic weight adjoint + fixed-order reduction of :688-780, fused
+ * into one pass over x, y, g.  Roles not set in `needed` are not written
+ * (their pointers may be NULL).  n_rows == 0 writes dw = 0.  dw is a
+ * fixed-order fp32 sum: bitwise reproducible for a given n_rows. */
+int o2mi_tp_backward_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
+                         const float *w, const float *g, float *dx, float *dy,
+                         float *dw, void *workspace, size_t workspace_bytes,
+                         int64_t n_rows, int needed, void *stream);
+
+/* Kernel timing for measurement harnesses (no counterpart in the reference):
+ * while enabled, every forward/backward call records a HIP event pair around
+ * its main kernel on the call's stream.  o2mi_kernel_timing_read waits for
+ * the recorded events and returns the summed milliseconds and counts since the
+ * previous read. */
+int o2mi_kernel_timing(int enable);
+int o2mi_kernel_timing_read(double *forward_ms, int *forward_count, double *backward_ms,
+                            int *backward_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ICTC_O2_HP_AMD_H */

@@ -1,0 +1,232 @@
+"""GPU parity of the HIP TensorProduct kernels against the fp64 oracle.
+
+Bar (the reference's gate, benchmarks/eqx/scripts/support.py:33-35 and
+validate_math.py:72-75): normalized max error <= 1e-5 for out, dx, dy and dw.
+Large shapes compare a random subset of rows for out / dx / dy (rows are
+independent) and obtain dw from a cotangent that is zero outside the subset,
+so the oracle's dw over that subset is the exact expected value while the
+kernels run with the full launch geometry.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import o2_oracle as O
+
+TOL = 1e-5
+
+pytestmark = pytest.mark.gpu
+
+
+def _module(channels, m_max, parity, normalization="component", layout_cls=None, seed=0):
+    from ictc_o2_hp import ComponentMajorTensorProduct, TensorProduct
+    torch.manual_seed(seed)
+    cls = layout_cls or TensorProduct
+    return cls(channels, m_max, parity=parity, normalization=normalization).cuda()
+
+
+def _run(module, x, y, g):
+    xt = torch.from_numpy(x).float().cuda().requires_grad_()
+    yt = torch.from_numpy(y).float().cuda().requires_grad_()
+    out = module(xt, yt)
+    dx, dy, dw = torch.autograd.grad(out, (xt, yt, module.weight),
+                                     torch.from_numpy(g).float().cuda())
+    torch.cuda.synchronize()
+    return [t.detach().double().cpu().numpy() for t in (out, dx, dy, dw)]
+
+
+def _check(plan, module, x, y, g, rows=None, layout=0):
+    print(f"case C={plan.C} M={plan.M} {plan.parity} {plan.normalization} N={x.shape[0]} "
+          f"layout={layout}", flush=True)
+    w = module.weight.detach().double().cpu().numpy()
+    if rows is not None:
+        g = g.copy()
+        mask = np.zeros(x.shape[0], bool)
+        mask[rows] = True
+        g[~mask] = 0.0
+    out, dx, dy, dw = _run(module, x, y, g)
+    sel = slice(None) if rows is None else rows
+    ref_out = O.forward(plan, x[sel], y[sel], w, layout)
+    ref_dx, ref_dy, ref_dw = O.backward(plan, x[sel], y[sel], w, g[sel], layout)
+    errors = {
+        "out": O.normalized_error(ref_out, out[sel]),
+        "dx": O.normalized_error(ref_dx, dx[sel]),
+        "dy": O.normalized_error(ref_dy, dy[sel]),
+        "dw": O.normalized_error(ref_dw, dw),
+    }
+    assert all(np.isfinite(a).all() for a in (out, dx, dy, dw))
+    assert max(errors.values()) <= TOL, errors
+    return errors
+
+
+CASES = [
+    # C, M, parity, normalization, N
+    (32, 2, "canonical", "component", 4096),   # configs[0] shape
+    (17, 3, "full", "component", 37),          # odd C, odd N (reproduction_check.json)
+    (32, 1, "canonical", "component", 37),
+    (32, 6, "full", "component", 37),
+    (4, 6, "full", "norm", 5),
+    (3, 1, "canonical", "norm", 1),
+    (2, 0, "full", "component", 9),
+    (5, 4, "canonical", "component", 300),     # odd C canonical: unaligned rows
+    (64, 4, "full", "component", 1000),
+    (130, 2, "full", "component", 70),         # 260 lanes: two tiles, partial second tile
+    (300, 1, "canonical", "component", 40),    # 300 lanes: two tiles
+    (256, 6, "full", "component", 33),         # 512 lanes, C256 m6 full
+]
+
+
+@pytest.mark.parametrize("channels,m_max,parity,normalization,n_rows", CASES)
+def test_parity_small(channels, m_max, parity, normalization, n_rows):
+    rng = np.random.default_rng(1000 + channels * 7 + m_max)
+    plan = O.OraclePlan(channels, m_max, parity, normalization)
+    module = _module(channels, m_max, parity, normalization)
+    x, y, g = (rng.standard_normal((n_rows, plan.width)) for _ in range(3))
+    _check(plan, module, x, y, g)
+
+
+def test_parity_config1_subset():
+    """C128, m6, full, N=6400 (checked on 512 random rows)."""
+    rng = np.random.default_rng(6400)
+    plan = O.OraclePlan(128, 6, "full")
+    module = _module(128, 6, "full")
+    x, y, g = (rng.standard_normal((6400, plan.width)) for _ in range(3))
+    rows = np.sort(rng.choice(6400, 512, replace=False))
+    _check(plan, module, x, y, g, rows=rows)
+
+
+@pytest.mark.parametrize("parity", ["canonical", "full"])
+def test_component_major_layouts(parity):
+    from ictc_o2_hp import ComponentMajorTensorProduct
+    rng = np.random.default_rng(77)
+    plan = O.OraclePlan(24, 3, parity)
+    module = _module(24, 3, parity, layout_cls=ComponentMajorTensorProduct)
+    x, y, g = (rng.standard_normal((150, plan.width)) for _ in range(3))
+    _check(plan, module, x, y, g, layout=1 if parity == "canonical" else 2)
+
+
+def test_golden_vectors(golden_tp):
+    """The reference's own fp64 outputs on stored inputs (tests/golden/tp_vectors.npz)."""
+    from ictc_o2_hp import TensorProduct
+    names = sorted({k.split("/")[0] for k in golden_tp.files})
+    for name in names:
+        c, m, parity, norm = name.split("_")
+        module = TensorProduct(int(c[1:]), int(m[1:]), parity=parity, normalization=norm).cuda()
+        with torch.no_grad():
+            module.weight.copy_(torch.from_numpy(golden_tp[f"{name}/weight"]).float())
+        got = _run(module, golden_tp[f"{name}/x"], golden_tp[f"{name}/y"],
+                   golden_tp[f"{name}/g"])
+        for key, value in zip(("out", "dx", "dy", "dw"), got):
+            err = O.normalized_error(golden_tp[f"{name}/{key}"], value)
+            assert err <= TOL, (name, key, err)
+
+
+def test_empty_rows():
+    module = _module(16, 3, "full")
+    x = torch.zeros(0, module.representation_dimension, device="cuda", requires_grad=True)
+    y = torch.zeros_like(x, requires_grad=True)
+    out = module(x, y)
+    assert out.shape == x.shape
+    dx, dy, dw = torch.autograd.grad(out, (x, y, module.weight), torch.zeros_like(out))
+    assert dx.shape == x.shape and dy.shape == y.shape
+    assert torch.count_nonzero(dw).item() == 0
+
+
+def test_backward_is_bitwise_reproducible():
+    module = _module(128, 6, "full")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(3000, module.representation_dimension, device="cuda", generator=gen)
+    y = torch.randn(x.shape, device="cuda", generator=gen)
+    g = torch.randn(x.shape, device="cuda", generator=gen)
+    results = []
+    for _ in range(3):
+        xt, yt = x.clone().requires_grad_(), y.clone().requires_grad_()
+        out = module(xt, yt)
+        results.append(torch.autograd.grad(out, (xt, yt, module.weight), g))
+    for other in results[1:]:
+        for a, b in zip(results[0], other):
+            assert torch.equal(a, b)
+
+
+def test_dw_additive_over_row_partitions():
+    """Full-size-style check: dw over all rows equals the sum of dw over a
+    partition of the rows, each computed with its own launch geometry."""
+    module = _module(64, 6, "full")
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    n = 20000
+    x = torch.randn(n, module.representation_dimension, device="cuda", generator=gen)
+    y = torch.randn(x.shape, device="cuda", generator=gen)
+    g = torch.randn(x.shape, device="cuda", generator=gen)
+
+    def dw_of(a, b, c):
+        a = a.clone().requires_grad_()
+        return torch.autograd.grad(module(a, b), module.weight, c)[0].double()
+
+    whole = dw_of(x, y, g)
+    parts = sum(dw_of(x[s:e], y[s:e], g[s:e]) for s, e in ((0, 7), (7, 5000), (5000, n)))
+    err = (whole - parts).abs().max().item() / max(whole.abs().max().item(), 1e-7)
+    assert err <= TOL, err
+
+
+def test_batch_shapes_and_noncontiguous():
+    from ictc_o2_hp import TensorProduct
+    torch.manual_seed(3)
+    module = TensorProduct(8, 2, parity="full").cuda()
+    w = module.representation_dimension
+    base = torch.randn(4, 6, 2 * w, device="cuda")
+    x = base[..., :w]          # non-contiguous view
+    y = torch.randn(4, 6, w, device="cuda")
+    out = module(x, y)
+    ref = module(x.contiguous().reshape(-1, w), y.reshape(-1, w)).reshape(4, 6, w)
+    assert out.shape == (4, 6, w)
+    assert torch.equal(out, ref)
+
+
+def test_torch_compile_fullgraph():
+    from ictc_o2_hp import TensorProduct
+    torch.manual_seed(4)
+    module = TensorProduct(32, 4, parity="full").cuda()
+    compiled = torch.compile(module, fullgraph=True, dynamic=False)
+    x = torch.randn(257, module.representation_dimension, device="cuda", requires_grad=True)
+    y = torch.randn_like(x, requires_grad=True)
+    g = torch.randn_like(x)
+    eager = torch.autograd.grad(module(x, y), (x, y, module.weight), g)
+    out = compiled(x, y)
+    comp = torch.autograd.grad(out, (x, y, module.weight), g)
+    for a, b in zip(eager, comp):
+        assert torch.allclose(a, b, rtol=0, atol=0)
+
+
+def test_double_backward_matches_fp64():
+    from ictc_o2_hp import TensorProduct
+    torch.manual_seed(6)
+    module = TensorProduct(6, 2, parity="full").cuda()
+    x = torch.randn(11, module.representation_dimension, device="cuda", requires_grad=True)
+    y = torch.randn_like(x, requires_grad=True)
+    out = module(x, y)
+    (gx,) = torch.autograd.grad(out.square().sum(), x, create_graph=True)
+    (hx,) = torch.autograd.grad(gx.sum(), y)
+    module64 = TensorProduct(6, 2, parity="full").double()
+    module64.weight.data.copy_(module.weight.data.double().cpu())
+    x64 = x.detach().double().cpu().requires_grad_()
+    y64 = y.detach().double().cpu().requires_grad_()
+    module64.internal_compute_dtype = torch.float64
+    out64 = module64(x64, y64)
+    (gx64,) = torch.autograd.grad(out64.square().sum(), x64, create_graph=True)
+    (hx64,) = torch.autograd.grad(gx64.sum(), y64)
+    assert O.normalized_error(hx64.numpy(), hx.double().cpu().numpy()) <= TOL
+
+
+def test_native_library_is_loaded():
+    """The GPU path must run the in-tree HIP library (no silent fallback)."""
+    from ictc_o2_hp import _native
+    lib = _native.library()
+    assert "ictc_o2_hp_amd" in lib.o2mi_version().decode()
+    module = _module(8, 1, "canonical")
+    x = torch.randn(3, module.representation_dimension, device="cuda")
+    module(x, x)
+    import os
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    assert _native.LIBRARY_NAME in maps
