@@ -1,0 +1,161 @@
+"""Drop-in API of the modules on the CPU (PyTorch algebra path)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import o2_oracle as O
+
+from conftest import GOLDEN
+
+
+def test_public_names():
+    import ictc_o2_hp
+    for name in ("TensorProduct", "TupleTensorProduct", "ComponentMajorTensorProduct",
+                 "ReferenceTensorProduct"):
+        assert getattr(ictc_o2_hp, name) is not None
+    assert ictc_o2_hp.__version__ == "0.1.6.dev0"
+
+
+@pytest.mark.parametrize("args", [(0, 2), (1.5, 2), (4, -1), (4, 1.5)])
+def test_constructor_validation(args):
+    from ictc_o2_hp import TensorProduct, ReferenceTensorProduct
+    for cls in (TensorProduct, ReferenceTensorProduct):
+        with pytest.raises(ValueError):
+            cls(*args)
+
+
+def test_bad_parity():
+    from ictc_o2_hp import TensorProduct
+    with pytest.raises(ValueError):
+        TensorProduct(4, 2, parity="odd")
+
+
+def test_width_errors():
+    from ictc_o2_hp import TensorProduct, ComponentMajorTensorProduct
+    for cls in (TensorProduct, ComponentMajorTensorProduct):
+        tp = cls(4, 2)
+        x = torch.randn(3, tp.representation_dimension)
+        with pytest.raises(ValueError):
+            tp(x[:, :-1], x[:, :-1])
+        with pytest.raises(ValueError):
+            tp(x, x[:2])
+
+
+def test_default_weights_match_reference_init():
+    """torch.manual_seed(0) then the per-path randn(out_mul) * 0.02 sequence
+    (native_o2.py:117), recorded from the reference."""
+    from ictc_o2_hp import TensorProduct
+    golden = np.load(GOLDEN / "default_weights.npz")
+    for c, m, parity in ((32, 2, "canonical"), (17, 3, "full"), (128, 6, "full")):
+        torch.manual_seed(0)
+        tp = TensorProduct(c, m, parity=parity)
+        assert np.array_equal(tp.weight.detach().numpy(), golden[f"C{c}_m{m}_{parity}"])
+
+
+def test_state_dict_layout():
+    """weight, cg_<p>, odd_to_even, even_to_odd persistent; routing not."""
+    from ictc_o2_hp import TensorProduct, ReferenceTensorProduct
+    tp = TensorProduct(8, 3, parity="full")
+    keys = set(tp.state_dict())
+    expected = {"weight", "odd_to_even", "even_to_odd"} | {f"cg_{p}" for p in range(len(tp.paths))}
+    assert keys == expected
+    assert tp.state_dict()["cg_0"].dtype == torch.float64
+    assert tp.weight.shape == (tp.parameter_count,)
+    ref = ReferenceTensorProduct(8, 3, parity="full")
+    rkeys = set(ref.state_dict())
+    assert rkeys == (expected - {"weight"}) | {f"weights.{p}" for p in range(len(ref.paths))}
+    tp.copy_weights_to_r5(ref)
+    other = TensorProduct(8, 3, parity="full")
+    other.load_weights_from_r5(ref)
+    assert torch.equal(other.weight, tp.weight)
+    with pytest.raises(ValueError):
+        TensorProduct(8, 2).copy_weights_to_r5(ref)
+
+
+def test_attributes():
+    from ictc_o2_hp import TensorProduct
+    tp = TensorProduct(128, 6, parity="full")
+    assert tp.representation_dimension == 3328
+    assert tp.parameter_count == 19712
+    assert len(tp.paths) == 85
+    assert len(tp.blocks) == 8 and tp.keys[0] == ("scalar", 1)
+    assert tp.representation_spec()[2]["labels"] == "1e+1o"
+
+
+@pytest.mark.parametrize("parity", ["canonical", "full"])
+def test_cpu_forward_and_vjp_match_oracle(parity):
+    from ictc_o2_hp import TensorProduct
+    torch.manual_seed(1)
+    tp = TensorProduct(6, 4, parity=parity)
+    plan = O.OraclePlan(6, 4, parity)
+    x = torch.randn(9, tp.representation_dimension, requires_grad=True)
+    y = torch.randn(9, tp.representation_dimension, requires_grad=True)
+    g = torch.randn(9, tp.representation_dimension)
+    out = tp(x, y)
+    grads = torch.autograd.grad(out, (x, y, tp.weight), g)
+    w = tp.weight.detach().double().numpy()
+    ref = [O.forward(plan, x.detach().numpy(), y.detach().numpy(), w),
+           *O.backward(plan, x.detach().numpy(), y.detach().numpy(), w, g.numpy())]
+    for r, a in zip(ref, [out, *grads]):
+        assert O.normalized_error(r, a.detach().double().numpy()) < 1e-6
+
+
+def test_tuple_flat_component_major_and_reference_agree():
+    from ictc_o2_hp import (ComponentMajorTensorProduct, ReferenceTensorProduct, TensorProduct,
+                            TupleTensorProduct)
+    torch.manual_seed(2)
+    flat = TensorProduct(5, 3, parity="full")
+    tup = TupleTensorProduct(5, 3, parity="full")
+    cm = ComponentMajorTensorProduct(5, 3, parity="full")
+    ref = ReferenceTensorProduct(5, 3, parity="full")
+    for m in (tup, cm):
+        m.weight.data.copy_(flat.weight.data)
+    flat.copy_weights_to_r5(ref)
+    x = torch.randn(4, flat.representation_dimension)
+    y = torch.randn(4, flat.representation_dimension)
+    out = flat(x, y)
+    blocks = lambda v: tuple(v[:, s:s + b.multiplicity * b.irrep_dimension]
+                             .reshape(4, b.multiplicity, b.irrep_dimension)
+                             for s, b in zip(flat._plan.key_offsets, flat.blocks))
+    tup_out = torch.cat([b.reshape(4, -1) for b in tup(blocks(x), blocks(y))], dim=-1)
+    ref_out = torch.cat([b.reshape(4, -1) for b in ref(blocks(x), blocks(y))], dim=-1)
+    cm_out = cm._unpack(cm(cm._pack(blocks(x)), cm._pack(blocks(y))))
+    cm_out = torch.cat([b.reshape(4, -1) for b in cm_out], dim=-1)
+    for other in (tup_out, ref_out, cm_out):
+        assert torch.allclose(out, other, rtol=1e-5, atol=1e-6)
+
+
+def test_double_module_uses_fp32_internal_compute_like_reference():
+    """native_o2.py:82 / fast_o2.py:87-95: the compute dtype stays float32."""
+    from ictc_o2_hp import TensorProduct
+    tp = TensorProduct(3, 2, parity="full").double()
+    x = torch.randn(2, tp.representation_dimension, dtype=torch.float64)
+    out = tp(x, x)
+    assert out.dtype == torch.float64
+    tp.internal_compute_dtype = torch.float64
+    out64 = tp(x, x)
+    assert (out - out64).abs().max() > 0
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from ictc_o2_hp import _native
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setenv("ICTC_O2_HP_AMD_LIBRARY", str(tmp_path / "absent.so"))
+    with pytest.raises(_native.NativeLibraryError):
+        _native.library()
+
+
+def test_o2_math_public_functions():
+    from ictc_o2_hp import o2_math
+    assert o2_math.o2_valid_output_keys("2", "2") == [("scalar", 1), ("scalar", -1), ("freq", 4)]
+    assert o2_math.o2_valid_output_keys("0o", "3") == [("freq", 3)]
+    cg = o2_math.o2_cg_tensor("0o", "1", "1")
+    assert torch.equal(cg[0], torch.tensor([[0.0, 1.0], [-1.0, 0.0]], dtype=torch.float64))
+    g = torch.tensor([[0.0, -1.0], [1.0, 0.0]], dtype=torch.float64)
+    rep = o2_math.o2_representation(g, "2")
+    assert torch.allclose(rep, torch.tensor([[-1.0, 0.0], [0.0, -1.0]], dtype=torch.float64),
+                          atol=1e-12)
+    with pytest.raises(ValueError):
+        o2_math.o2_cg_tensor("0x", "1", "1")
