@@ -105,22 +105,24 @@ int pick_variant(const o2mi_tp_plan* p, std::initializer_list<const void*> ptrs)
 }
 
 // Rows and lanes per block, rows per block, and the grid for `n_rows` rows
-// when at most `target_blocks` blocks should be resident.
-o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_blocks, int* grid) {
+// when at most `target_blocks` blocks should be resident and a block covers at
+// most `tile` lanes of a row.
+o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_blocks, int tile,
+                      int* grid) {
   o2mi::TPGeom g{};
   g.n_rows = n_rows;
   g.channels = p->channels;
   g.width = (int)p->width;
   g.weight_numel = (int)p->weight_numel;
   g.lanes = p->full ? 2 * p->channels : p->channels;
-  if (g.lanes <= o2mi::kBlock) {
+  if (g.lanes <= tile) {
     g.tile_lanes = g.lanes;
     g.rows_per_iter = o2mi::kBlock / g.lanes;
     g.tiles = 1;
   } else {
-    g.tile_lanes = o2mi::kBlock;
-    g.rows_per_iter = 1;
-    g.tiles = (g.lanes + o2mi::kBlock - 1) / o2mi::kBlock;
+    g.tile_lanes = tile;
+    g.rows_per_iter = o2mi::kBlock / tile;
+    g.tiles = (g.lanes + tile - 1) / tile;
   }
   const int64_t r = g.rows_per_iter;
   const int64_t iterations = std::max<int64_t>(1, (n_rows + r - 1) / r);
@@ -128,7 +130,12 @@ o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_bloc
   const int64_t groups = std::min(max_groups, iterations);
   const int64_t iters_per_group = (iterations + groups - 1) / groups;
   g.rows_per_group = iters_per_group * r;
-  const int64_t used_groups = (iterations + iters_per_group - 1) / iters_per_group;
+  // Contiguous order: every group gets iters_per_group iterations; strided
+  // order: groups take iterations round-robin.
+  const int64_t used_groups = O2MI_ROW_ORDER == 1
+                                  ? groups
+                                  : (iterations + iters_per_group - 1) / iters_per_group;
+  g.groups = used_groups;
   *grid = (int)(used_groups * g.tiles);
   return g;
 }
@@ -146,7 +153,7 @@ BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant)
   BackwardShape s{};
   s.variant = variant;
   const int64_t target = (int64_t)p->set->blocks_per_cu(variant, true) * device_cus();
-  s.geom = geometry(p, n_rows, target, &s.grid);
+  s.geom = geometry(p, n_rows, target, o2mi::kBackwardTile, &s.grid);
   s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
   s.splits = s.partial_rows <= kReduceSplitRows
                  ? 1
@@ -355,12 +362,29 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
   const int variant = pick_variant(plan, {x, y, out});
   const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
   int grid = 0;
-  const o2mi::TPGeom g = geometry(plan, n_rows, target, &grid);
+  const o2mi::TPGeom g = geometry(plan, n_rows, target, o2mi::kForwardTile, &grid);
   TimedLaunch timed;
   const bool timing = timing_begin(s, &timed, 0);
   const hipError_t err = plan->set->forward(variant, x, y, w, out, g, grid, s);
   if (timing) timing_end(s, &timed);
   if (err != hipSuccess) return fail_hip(err, "tp forward launch");
+  return O2MI_OK;
+}
+
+int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward, int* grid,
+                         int* blocks_per_cu, int* rows_per_iter, int* tiles) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "bad plan or n_rows");
+  const int variant = plan->layout == O2MI_LAYOUT_CHANNEL_MAJOR ? o2mi::kVariantChannelMajorVec2
+                                                                : o2mi::kVariantComponentMajor;
+  const int per_cu = plan->set->blocks_per_cu(variant, backward != 0);
+  int g = 0;
+  const o2mi::TPGeom geom =
+      geometry(plan, n_rows, (int64_t)per_cu * device_cus(),
+               backward ? o2mi::kBackwardTile : o2mi::kForwardTile, &g);
+  if (grid) *grid = g;
+  if (blocks_per_cu) *blocks_per_cu = per_cu;
+  if (rows_per_iter) *rows_per_iter = geom.rows_per_iter;
+  if (tiles) *tiles = geom.tiles;
   return O2MI_OK;
 }
 

@@ -58,7 +58,37 @@ struct TermSpec {
   int sign;     // +1 or -1
 };
 
+// Build-time tuning knobs (defaults are the measured best).
+#ifndef O2MI_LOAD_CPOL
+#define O2MI_LOAD_CPOL 0  // cache-policy bits of row loads (1 sc0, 2 nt, 16 sc1)
+#endif
+#ifndef O2MI_STORE_CPOL
+#define O2MI_STORE_CPOL 2  // cache-policy bits of row stores: non-temporal
+#endif
+#ifndef O2MI_FWD_PREFETCH
+#define O2MI_FWD_PREFETCH 0  // forward loads the next iteration's rows early
+#endif
+#ifndef O2MI_FWD_WAVES
+#define O2MI_FWD_WAVES 1  // minimum waves per SIMD requested for the forward
+#endif
+#ifndef O2MI_BWD_WAVES
+#define O2MI_BWD_WAVES 2  // minimum waves per SIMD requested for the backward
+#endif
+#ifndef O2MI_FWD_TILE
+#define O2MI_FWD_TILE 256  // lanes of one row handled by a forward block
+#endif
+#ifndef O2MI_BWD_TILE
+#define O2MI_BWD_TILE 256  // lanes of one row handled by a backward block
+#endif
+#ifndef O2MI_ROW_ORDER
+#define O2MI_ROW_ORDER 1  // 1: block b takes iterations b, b+G, ...; 0: one contiguous range
+#endif
+
 constexpr int kBlock = 256;
+constexpr int kForwardTile = O2MI_FWD_TILE;
+constexpr int kBackwardTile = O2MI_BWD_TILE;
+static_assert(kForwardTile % 2 == 0 && kForwardTile <= kBlock, "tile must be even, <= block");
+static_assert(kBackwardTile % 2 == 0 && kBackwardTile <= kBlock, "tile must be even, <= block");
 // Byte offset given to lanes with nothing to load or store: beyond any
 // descriptor size used here (< 2^31), with room to add key offsets.
 constexpr uint32_t kIdle = 0x80000000u;
@@ -75,38 +105,35 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Launch geometry, computed on the host (o2mi_capi.hip).
 struct TPGeom {
   int64_t n_rows;
-  int64_t rows_per_group;  // rows owned by one block (multiple of rows_per_iter)
+  int64_t rows_per_group;  // contiguous order: rows owned by one block (multiple of rows_per_iter)
+  int64_t groups;          // blocks along the rows (grid = groups * tiles)
   int channels;            // C
   int width;               // W, floats per row
   int lanes;               // lanes per row: 2C (full) or C (canonical)
-  int tile_lanes;          // lanes of one row handled by a block: min(lanes, 256)
+  int tile_lanes;          // lanes of one row handled by a block: min(lanes, tile)
   int rows_per_iter;       // rows a block advances per iteration
-  int tiles;               // blocks sharing one row range: ceil(lanes / 256)
+  int tiles;               // blocks sharing one row range: ceil(lanes / tile)
   int weight_numel;        // P_w
 };
 
 struct Lane {
   int c;     // channel (clamped to 0 on idle lanes)
   int q;     // copy (always 0 for canonical parity)
+  int jloc;  // lane index inside the block's tile (2 cloc + q for full parity)
   int cloc;  // channel index inside the block's tile
   int slot;  // row slot inside one iteration
   bool active;
 };
 
-template <bool kFull>
+template <bool kFull, int kTile>
 __device__ __forceinline__ Lane make_lane(const TPGeom& g, int tile) {
   Lane l;
   const int t = threadIdx.x;
-  int jloc;
-  if (g.tiles == 1) {
-    l.slot = t / g.tile_lanes;
-    jloc = t - l.slot * g.tile_lanes;
-  } else {
-    l.slot = 0;
-    jloc = t;
-  }
-  const int j = tile * kBlock + jloc;
+  l.slot = t / g.tile_lanes;
+  const int jloc = t - l.slot * g.tile_lanes;
+  const int j = tile * kTile + jloc;
   l.active = l.slot < g.rows_per_iter && j < g.lanes;
+  l.jloc = jloc;
   const int jj = l.active ? j : 0;
   l.c = kFull ? (jj >> 1) : jj;
   l.q = kFull ? (jj & 1) : 0;
@@ -140,7 +167,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, i
 }
 
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, 0));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, O2MI_LOAD_CPOL));
 }
 
 using f32x2 = float __attribute__((ext_vector_type(2)));
@@ -150,14 +178,16 @@ using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 // single vector element (both elements read as element 0).
 __device__ __forceinline__ void bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff,
                                        float& a, float& b) {
-  const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, 0));
+  const f32x2 v = __builtin_bit_cast(
+      f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, O2MI_LOAD_CPOL));
   a = v.x;
   b = v.y;
 }
 
 __device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff,
                                        int soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, soff,
+                                        O2MI_STORE_CPOL);
 }
 
 __device__ __forceinline__ void bstore2(__amdgpu_buffer_rsrc_t r, float a, float b,
@@ -165,7 +195,8 @@ __device__ __forceinline__ void bstore2(__amdgpu_buffer_rsrc_t r, float a, float
   f32x2 v;
   v.x = a;
   v.y = b;
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)voff, soff,
+                                        O2MI_STORE_CPOL);
 }
 
 // Exchange a value between the two lanes of a copy pair (quad_perm 1,0,3,2).
@@ -276,46 +307,139 @@ constexpr bool out_is_freq(int p) {
   return P::keys[P::paths[p].k3].dim == 2;
 }
 
-// Rows of iteration `it` that exist: the descriptor covers exactly these.
-__device__ __forceinline__ int iteration_rows(const TPGeom& g, int64_t r0, int64_t r1, int it) {
-  const int64_t left = r1 - (r0 + (int64_t)it * g.rows_per_iter);
-  return left <= 0 ? 0 : (left < g.rows_per_iter ? (int)left : g.rows_per_iter);
+
+// ---------------------------------------------------------------------------
+// Path weights, times each path's coupling magnitude, staged in LDS for the
+// block's tile: path p starts at wunits * U floats (U = kTile / 2 for full
+// parity, kTile for canonical).  Frequency-output paths of full parity hold
+// both copies interleaved by lane (index 2 c + q), so neighbouring lanes read
+// neighbouring banks; scalar-output paths hold one value per channel.
+template <class P, int kTile>
+constexpr int lds_unit() {
+  return P::kFull ? kTile / 2 : kTile;
+}
+
+template <class P, int kTile>
+constexpr size_t lds_bytes() {
+  return sizeof(float) * (size_t)P::kUnits * (size_t)lds_unit<P, kTile>();
+}
+
+template <class P, int kTile>
+__device__ __forceinline__ void stage_weights(float* lds, const float* __restrict__ w, int C,
+                                              int tile) {
+  constexpr int U = lds_unit<P, kTile>();
+  const int c0 = tile * U;
+  const int t = threadIdx.x;
+  static_for<P::kPaths>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr PathSpec ps = P::paths[p];
+    if constexpr (P::kFull && out_is_freq<P>(p)) {
+      if (t < kTile) {
+        const int c = c0 + (t >> 1);
+        lds[ps.wunits * U + t] = c < C ? w[(ps.wunits + (t & 1)) * C + c] * ps.mag : 0.f;
+      }
+    } else {
+      if (t < U) {
+        const int c = c0 + t;
+        lds[ps.wunits * U + t] = c < C ? w[ps.wunits * C + c] * ps.mag : 0.f;
+      }
+    }
+  });
+}
+
+// LDS column of this lane for frequency-output and scalar-output paths.
+template <class P>
+struct WeightColumns {
+  int freq, scalar;
+};
+
+template <class P>
+__device__ __forceinline__ WeightColumns<P> weight_columns(const Lane& l) {
+  return {P::kFull ? l.jloc : l.cloc, l.cloc};
+}
+
+template <class P, int kTile, int kPath>
+__device__ __forceinline__ float staged_weight(const float* lds, const WeightColumns<P>& col) {
+  constexpr PathSpec ps = P::paths[kPath];
+  constexpr int U = lds_unit<P, kTile>();
+  return lds[(out_is_freq<P>(kPath) ? col.freq : col.scalar) + ps.wunits * U];
+}
+
+// Rows visited by one block.  Iteration `it` covers rows [row0(it),
+// row0(it) + rows(it)); the buffer descriptors cover exactly those rows.
+// Strided order keeps all blocks inside one contiguous window of the tensors
+// at any time (page and DRAM locality); the contiguous order gives each block
+// one range.  Either way the assignment is fixed, so dw is reproducible.
+struct RowSchedule {
+  int64_t first, step, limit;
+  int iters;
+  int rows_per_iter;
+
+  __device__ __forceinline__ int64_t row0(int it) const { return first + (int64_t)it * step; }
+  __device__ __forceinline__ int rows(int it) const {
+    const int64_t left = limit - row0(it);
+    return left <= 0 ? 0 : (left < rows_per_iter ? (int)left : rows_per_iter);
+  }
+};
+
+__device__ __forceinline__ RowSchedule row_schedule(const TPGeom& g, int64_t group) {
+  RowSchedule s;
+  s.rows_per_iter = g.rows_per_iter;
+  if constexpr (O2MI_ROW_ORDER == 1) {
+    s.first = group * g.rows_per_iter;
+    s.step = g.groups * g.rows_per_iter;
+    s.limit = g.n_rows;
+    s.iters = s.first < g.n_rows ? (int)((g.n_rows - s.first + s.step - 1) / s.step) : 0;
+  } else {
+    s.first = group * g.rows_per_group;
+    s.step = g.rows_per_iter;
+    s.limit = min(g.n_rows, s.first + g.rows_per_group);
+    s.iters = s.limit > s.first ? (int)((s.limit - s.first + s.step - 1) / s.step) : 0;
+  }
+  return s;
 }
 
 // ---------------------------------------------------------------------------
 // Forward: out = sum over paths of w * CG(x, y)  (native_o2.py:209-221).
-// Weights (times the path magnitude) are held in registers for all rows.
 template <class P, int kLayout, bool kVec2>
-__global__ __launch_bounds__(kBlock) void tp_forward_kernel(const float* __restrict__ x,
-                                                           const float* __restrict__ y,
-                                                           const float* __restrict__ w,
-                                                           float* __restrict__ out, TPGeom g) {
+__global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
+    float* __restrict__ out, TPGeom g) {
+  constexpr int kTile = kForwardTile;
+  extern __shared__ float lds_w[];
   const int tile = blockIdx.x % g.tiles;
   const int64_t group = blockIdx.x / g.tiles;
-  const Lane l = make_lane<P::kFull>(g, tile);
+  const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
+  stage_weights<P, kTile>(lds_w, w, C, tile);
+  __syncthreads();
+  WeightColumns<P> col = weight_columns<P>(l);
 
-  float wr[P::kPaths];
-  static_for<P::kPaths>([&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    constexpr PathSpec ps = P::paths[p];
-    const int oc = ((out_is_freq<P>(p) && P::kFull) ? l.q * C : 0) + l.c;
-    wr[p] = l.active ? w[ps.wunits * C + oc] * ps.mag : 0.f;
-  });
-
-  const int64_t r0 = group * g.rows_per_group;
-  const int64_t r1 = min(g.n_rows, r0 + g.rows_per_group);
-  const int iters = r1 > r0 ? (int)((r1 - r0 + g.rows_per_iter - 1) / g.rows_per_iter) : 0;
-  for (int it = 0; it < iters; ++it) {
-    const int64_t row0 = r0 + (int64_t)it * g.rows_per_iter;
-    const int rows = iteration_rows(g, r0, r1, it);
-    const auto rx = rows_rsrc(x, row0, g.width, rows);
-    const auto ry = rows_rsrc(y, row0, g.width, rows);
-    const auto ro = rows_rsrc(out, row0, g.width, rows);
-    float X[P::kKeys][2], Y[P::kKeys][2];
-    load_row<P, kLayout, kVec2>(rx, C, l, o, false, X);
-    load_row<P, kLayout, kVec2>(ry, C, l, o, false, Y);
+  const RowSchedule sched = row_schedule(g, group);
+  float X[P::kKeys][2], Y[P::kKeys][2];
+  if constexpr (O2MI_FWD_PREFETCH) {
+    load_row<P, kLayout, kVec2>(rows_rsrc(x, sched.row0(0), g.width, sched.rows(0)), C, l, o,
+                                false, X);
+    load_row<P, kLayout, kVec2>(rows_rsrc(y, sched.row0(0), g.width, sched.rows(0)), C, l, o,
+                                false, Y);
+  }
+  for (int it = 0; it < sched.iters; ++it) {
+    const int64_t row0 = sched.row0(it);
+    const int rows = sched.rows(it);
+    float Xn[P::kKeys][2], Yn[P::kKeys][2];
+    if constexpr (O2MI_FWD_PREFETCH) {
+      const int64_t row_next = sched.row0(it + 1);
+      const int rows_next = sched.rows(it + 1);
+      load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
+      load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
+    } else {
+      load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
+      load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
+    }
+    // Re-read the weights every iteration: keeping all of them in registers
+    // would cost occupancy.
+    asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
     float A[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       A[decltype(kc)::value][0] = 0.f;
@@ -324,12 +448,22 @@ __global__ __launch_bounds__(kBlock) void tp_forward_kernel(const float* __restr
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
+      const float wv = staged_weight<P, kTile, p>(lds_w, col);
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
-      A[ps.k3][0] = fmaf(wr[p], f0, A[ps.k3][0]);
-      if constexpr (out_is_freq<P>(p)) A[ps.k3][1] = fmaf(wr[p], f1, A[ps.k3][1]);
+      A[ps.k3][0] = fmaf(wv, f0, A[ps.k3][0]);
+      if constexpr (out_is_freq<P>(p)) A[ps.k3][1] = fmaf(wv, f1, A[ps.k3][1]);
     });
-    store_row<P, kLayout, kVec2>(ro, C, l, o, A);
+    store_row<P, kLayout, kVec2>(rows_rsrc(out, row0, g.width, rows), C, l, o, A);
+    if constexpr (O2MI_FWD_PREFETCH) {
+      static_for<P::kKeys>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        X[k][0] = Xn[k][0];
+        X[k][1] = Xn[k][1];
+        Y[k][0] = Yn[k][0];
+        Y[k][1] = Yn[k][1];
+      });
+    }
   }
 }
 
@@ -338,56 +472,27 @@ __global__ __launch_bounds__(kBlock) void tp_forward_kernel(const float* __restr
 //   dx[k1][i] += w * coef * g[k3][k] * y[k2][j]       (triton_o2.py:452-501)
 //   dy[k2][j] += w * coef * g[k3][k] * x[k1][i]
 //   dw[p, o]  += coef * x[k1][i] * y[k2][j] * g[k3][k] (triton_o2.py:571-607)
-// Weights times magnitudes are staged in LDS as [weight unit][kStride] with
-// kStride = 128 (full: channels per 256-lane tile) or 256 (canonical).  The
-// next iteration's rows are loaded while the current one is computed.
-template <class P>
-constexpr int lds_stride() {
-  return P::kFull ? kBlock / 2 : kBlock;
-}
-
-template <class P>
-constexpr size_t backward_lds_bytes() {
-  return sizeof(float) * (size_t)P::kUnits * (size_t)lds_stride<P>();
-}
-
+// The next iteration's rows are loaded while the current one is computed.
 template <class P, int kLayout, bool kVec2>
-__global__ __launch_bounds__(kBlock, 2) void tp_backward_kernel(
+__global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ gout, float* __restrict__ dx, float* __restrict__ dy,
     float* __restrict__ partial, TPGeom g, int needed) {
-  constexpr int kStride = lds_stride<P>();
+  constexpr int kTile = kBackwardTile;
   extern __shared__ float lds_w[];
   const int tile = blockIdx.x % g.tiles;
   const int64_t group = blockIdx.x / g.tiles;
-  const Lane l = make_lane<P::kFull>(g, tile);
+  const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
-
-  // Stage this tile's weights: unit u, column col <-> w[u * C + c0 + col].
-  {
-    const int c0 = tile * kStride;
-    const int col = threadIdx.x;
-    static_for<P::kUnits>([&](auto uc) {
-      constexpr int u = decltype(uc)::value;
-      if (col < kStride) {
-        const int c = c0 + col;
-        lds_w[u * kStride + col] = c < C ? w[u * C + c] * P::unit_mag[u] : 0.f;
-      }
-    });
-  }
+  stage_weights<P, kTile>(lds_w, w, C, tile);
   __syncthreads();
-
-  // Per-lane LDS columns of frequency-output and scalar-output weights.
-  int col_freq = (P::kFull ? l.q * kStride : 0) + l.cloc;
-  int col_scalar = l.cloc;
+  WeightColumns<P> col = weight_columns<P>(l);
 
   float dwacc[P::kPaths];
   static_for<P::kPaths>([&](auto pc) { dwacc[decltype(pc)::value] = 0.f; });
 
-  const int64_t r0 = group * g.rows_per_group;
-  const int64_t r1 = min(g.n_rows, r0 + g.rows_per_group);
-  const int iters = r1 > r0 ? (int)((r1 - r0 + g.rows_per_iter - 1) / g.rows_per_iter) : 0;
+  const RowSchedule sched = row_schedule(g, group);
   // Stores of roles that were not requested go to idle offsets (dropped).
   LaneOffsets ox = o, oy = o;
   if (!(needed & 1)) ox.scalar_own = ox.freq = kIdle;
@@ -395,18 +500,19 @@ __global__ __launch_bounds__(kBlock, 2) void tp_backward_kernel(
 
   float X[P::kKeys][2], Y[P::kKeys][2], G[P::kKeys][2];
   {
-    const int rows = iteration_rows(g, r0, r1, 0);
-    load_row<P, kLayout, kVec2>(rows_rsrc(x, r0, g.width, rows), C, l, o, false, X);
-    load_row<P, kLayout, kVec2>(rows_rsrc(y, r0, g.width, rows), C, l, o, false, Y);
+    const int64_t row0 = sched.row0(0);
+    const int rows = sched.rows(0);
+    load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
+    load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
     // Scalar outputs belong to the copy-0 lane; the copy-1 lane reads a zero
     // cotangent there, which removes its (wrong-copy) contributions.
-    load_row<P, kLayout, kVec2>(rows_rsrc(gout, r0, g.width, rows), C, l, o, true, G);
+    load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
   }
-  for (int it = 0; it < iters; ++it) {
-    const int64_t row0 = r0 + (int64_t)it * g.rows_per_iter;
-    const int rows = iteration_rows(g, r0, r1, it);
-    const int64_t row_next = row0 + g.rows_per_iter;
-    const int rows_next = iteration_rows(g, r0, r1, it + 1);
+  for (int it = 0; it < sched.iters; ++it) {
+    const int64_t row0 = sched.row0(it);
+    const int rows = sched.rows(it);
+    const int64_t row_next = sched.row0(it + 1);
+    const int rows_next = sched.rows(it + 1);
     float Xn[P::kKeys][2], Yn[P::kKeys][2], Gn[P::kKeys][2];
     load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
     load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
@@ -417,14 +523,14 @@ __global__ __launch_bounds__(kBlock, 2) void tp_backward_kernel(
       constexpr int k = decltype(kc)::value;
       DX[k][0] = DX[k][1] = DY[k][0] = DY[k][1] = 0.f;
     });
-    // Re-read the weights from LDS every iteration: hoisting the 85-odd
-    // loop-invariant reads out of the loop would cost as many registers.
-    asm volatile("" : "+v"(col_freq), "+v"(col_scalar));
+    // Re-read the weights from LDS every iteration: hoisting the loop-invariant
+    // reads out of the loop would cost as many registers.
+    asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
       constexpr bool freq3 = out_is_freq<P>(p);
-      const float wv = lds_w[(freq3 ? col_freq : col_scalar) + ps.wunits * kStride];
+      const float wv = staged_weight<P, kTile, p>(lds_w, col);
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       dwacc[p] = fmaf(G[ps.k3][0], f0, dwacc[p]);

@@ -56,7 +56,12 @@ inline hipError_t allow_lds(const void* kernel, size_t bytes, std::atomic<uint64
 template <class P, int kLayout, bool kVec2>
 hipError_t launch_forward(const float* x, const float* y, const float* w, float* out,
                           const TPGeom& g, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), 0,
+  static std::atomic<uint64_t> done{0};
+  const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
+  const size_t lds = lds_bytes<P, kForwardTile>();
+  hipError_t err = allow_lds(kernel, lds, done);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
                      stream, x, y, w, out, g);
   return hipGetLastError();
 }
@@ -67,7 +72,7 @@ hipError_t launch_backward(const float* x, const float* y, const float* w, const
                            int needed, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-  const size_t lds = backward_lds_bytes<P>();
+  const size_t lds = lds_bytes<P, kBackwardTile>();
   hipError_t err = allow_lds(kernel, lds, done);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((tp_backward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
@@ -105,17 +110,20 @@ hipError_t backward_dispatch(int variant, const float* x, const float* y, const 
 template <class P, int kLayout, bool kVec2>
 int occupancy_of(bool backward) {
   int blocks = 0;
+  static std::atomic<uint64_t> done_f{0}, done_b{0};
   if (backward) {
     const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-    static std::atomic<uint64_t> done{0};
-    if (allow_lds(kernel, backward_lds_bytes<P>(), done) != hipSuccess) return 1;
+    const size_t lds = lds_bytes<P, kBackwardTile>();
+    if (allow_lds(kernel, lds, done_b) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBlock,
-            backward_lds_bytes<P>()) != hipSuccess)
+            &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
       return 1;
   } else {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, tp_forward_kernel<P, kLayout, kVec2>,
-                                                    kBlock, 0) != hipSuccess)
+    const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
+    const size_t lds = lds_bytes<P, kForwardTile>();
+    if (allow_lds(kernel, lds, done_f) != hipSuccess) return 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
       return 1;
   }
   return blocks > 0 ? blocks : 1;

@@ -52,6 +52,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_tp_backward_workspace_bytes.argtypes = [vp, c_i64]
     lib.o2mi_tp_backward_f32.restype = c_int
     lib.o2mi_tp_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, vp, c_sz, c_i64, c_int, vp]
+    lib.o2mi_tp_launch_shape.restype = c_int
+    lib.o2mi_tp_launch_shape.argtypes = [vp, c_i64, c_int] + [ctypes.POINTER(c_int)] * 4
     lib.o2mi_kernel_timing.restype = c_int
     lib.o2mi_kernel_timing.argtypes = [c_int]
     lib.o2mi_kernel_timing_read.restype = c_int
@@ -112,6 +114,15 @@ class TPNativePlan:
     def forward(self, x, y, w, out, n_rows: int, stream: int) -> None:
         check(self._lib.o2mi_tp_forward_f32(self.handle, x, y, w, out, n_rows, stream),
               "o2mi_tp_forward_f32")
+
+    def launch_shape(self, n_rows: int, backward: bool) -> dict:
+        """Grid, resident blocks per CU, rows per iteration, tiles (needs a GPU)."""
+        vals = [ctypes.c_int() for _ in range(4)]
+        check(self._lib.o2mi_tp_launch_shape(self.handle, n_rows, int(backward),
+                                             *[ctypes.byref(v) for v in vals]),
+              "o2mi_tp_launch_shape")
+        return dict(zip(("grid", "blocks_per_cu", "rows_per_iter", "tiles"),
+                        (v.value for v in vals)))
 
     def workspace_bytes(self, n_rows: int) -> int:
         return int(self._lib.o2mi_tp_backward_workspace_bytes(self.handle, n_rows))

@@ -75,6 +75,13 @@ int o2mi_tp_table(int m_max, int parity, int normalization, int *n_paths,
 int o2mi_tp_forward_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
                         const float *w, float *out, int64_t n_rows, void *stream);
 
+/* Launch shape the library picks on the current device for n_rows rows of a
+ * forward (backward = 0) or backward (1) call: grid blocks, resident blocks per
+ * CU assumed, rows per block iteration and blocks per row (channel tiles).
+ * No counterpart in the reference (its grids are fixed per op). */
+int o2mi_tp_launch_shape(const o2mi_tp_plan *plan, int64_t n_rows, int backward, int *grid,
+                         int *blocks_per_cu, int *rows_per_iter, int *tiles);
+
 /* Bytes of workspace o2mi_tp_backward_f32 needs for n_rows rows. */
 size_t o2mi_tp_backward_workspace_bytes(const o2mi_tp_plan *plan, int64_t n_rows);
 
