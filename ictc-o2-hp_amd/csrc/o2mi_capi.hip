@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "ictc_o2_hp_amd.h"
+#include "o2mi_error.hpp"
 #include "o2mi_tp_launch.hpp"
 
 // Defined by the generated registry (one entry per compiled plan).
@@ -27,17 +28,20 @@ struct o2mi_tp_plan {
   int64_t weight_numel;
 };
 
+std::string& o2mi_error_slot() {
+  thread_local std::string message;
+  return message;
+}
+
 namespace {
 
-thread_local std::string g_last_error;
-
 int fail(int status, const std::string& message) {
-  g_last_error = message;
+  o2mi_error_slot() = message;
   return status;
 }
 
 int fail_hip(hipError_t err, const char* where) {
-  g_last_error = std::string(where) + ": " + hipGetErrorString(err);
+  o2mi_error_slot() = std::string(where) + ": " + hipGetErrorString(err);
   return O2MI_ERR_HIP;
 }
 
@@ -264,7 +268,7 @@ int o2mi_kernel_timing_read(double* forward_ms, int* forward_count, double* back
   return status;
 }
 
-const char* o2mi_last_error(void) { return g_last_error.c_str(); }
+const char* o2mi_last_error(void) { return o2mi_error_slot().c_str(); }
 
 const char* o2mi_version(void) { return "ictc_o2_hp_amd 0.1.0 (gfx950)"; }
 

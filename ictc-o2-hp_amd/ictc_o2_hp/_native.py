@@ -28,6 +28,17 @@ class NativeLibraryError(RuntimeError):
     """The HIP extension is missing, failed to load or reported an error."""
 
 
+class UvuProblem(ctypes.Structure):
+    """o2mi_uvu_problem of include/ictc_o2_hp_amd.h."""
+    _fields_ = [("n_rows", ctypes.c_int64), ("channels", ctypes.c_int32),
+                ("channels_in2", ctypes.c_int32), ("n_paths", ctypes.c_int32),
+                ("n_out_entries", ctypes.c_int32), ("n_in2_entries", ctypes.c_int32),
+                ("width1", ctypes.c_int32), ("width2", ctypes.c_int32),
+                ("shared_weights", ctypes.c_int32), ("info", ctypes.c_void_p),
+                ("coefficients", ctypes.c_void_p), ("first_order", ctypes.c_void_p),
+                ("second_order", ctypes.c_void_p)]
+
+
 def _declare(lib: ctypes.CDLL) -> None:
     c_int, c_i64, c_sz, vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
     fp = ctypes.c_void_p
@@ -52,6 +63,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_tp_backward_workspace_bytes.argtypes = [vp, c_i64]
     lib.o2mi_tp_backward_f32.restype = c_int
     lib.o2mi_tp_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, vp, c_sz, c_i64, c_int, vp]
+    prob = ctypes.POINTER(UvuProblem)
+    lib.o2mi_uvu_forward_f32.restype = c_int
+    lib.o2mi_uvu_forward_f32.argtypes = [prob, fp, fp, fp, fp, vp]
+    lib.o2mi_uvu_backward_workspace_bytes.restype = c_sz
+    lib.o2mi_uvu_backward_workspace_bytes.argtypes = [prob, c_int]
+    lib.o2mi_uvu_backward_f32.restype = c_int
+    lib.o2mi_uvu_backward_f32.argtypes = [prob, fp, fp, fp, fp, fp, fp, fp, c_int, vp, c_sz, vp]
     lib.o2mi_tp_launch_shape.restype = c_int
     lib.o2mi_tp_launch_shape.argtypes = [vp, c_i64, c_int] + [ctypes.POINTER(c_int)] * 4
     lib.o2mi_kernel_timing.restype = c_int

@@ -96,6 +96,42 @@ int o2mi_tp_backward_f32(const o2mi_tp_plan *plan, const float *x, const float *
                          float *dw, void *workspace, size_t workspace_bytes,
                          int64_t n_rows, int needed, void *stream);
 
+/* ---- uvu product (UvuTensorProduct) ---------------------------------------
+ * One problem description per call; the tables are device arrays the caller
+ * owns (the module buffers _path_info, _coefficients, _first_order,
+ * _second_order of uvu_o2.py:218-226, built as in uvu_triton.py:39-67). */
+typedef struct o2mi_uvu_problem {
+  int64_t n_rows;
+  int32_t channels;       /* C: channels per entry of the first input and output */
+  int32_t channels_in2;   /* V: channels per entry of the second input */
+  int32_t n_paths;        /* P */
+  int32_t n_out_entries;  /* entries of the first input (= output entries) */
+  int32_t n_in2_entries;  /* entries of the second input */
+  int32_t width1;         /* floats per row of x and out */
+  int32_t width2;         /* floats per row of y */
+  int32_t shared_weights; /* 1: w is [P*C*V]; 0: w is [n_rows, P*C*V] */
+  const int32_t *info;         /* [P + 2*n_out_entries + n_in2_entries][7] records */
+  const float *coefficients;   /* [P][2][2][2]: out, in1, in2 components */
+  const int32_t *first_order;  /* [P] paths sorted by first entry */
+  const int32_t *second_order; /* [P] paths sorted by second entry */
+} o2mi_uvu_problem;
+
+/* out = uvu(x, y; w).  Replaces the uvu forward / forward_into ops
+ * (uvu_triton.py:235-284). */
+int o2mi_uvu_forward_f32(const o2mi_uvu_problem *problem, const float *x, const float *y,
+                         const float *w, float *out, void *stream);
+
+/* Workspace of o2mi_uvu_backward_f32 (non-zero only for shared weights with
+ * the weight role requested). */
+size_t o2mi_uvu_backward_workspace_bytes(const o2mi_uvu_problem *problem, int needed);
+
+/* (gx, gy, gw) for the roles in `needed` (1 x, 2 y, 4 w).  Replaces the uvu
+ * backward / backward_into ops (uvu_triton.py:287-414).  gw is [P*C*V] for
+ * shared weights (a fixed-order sum over rows) or [n_rows, P*C*V]. */
+int o2mi_uvu_backward_f32(const o2mi_uvu_problem *problem, const float *x, const float *y,
+                          const float *w, const float *g, float *gx, float *gy, float *gw,
+                          int needed, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Kernel timing for measurement harnesses (no counterpart in the reference):
  * while enabled, every forward/backward call records a HIP event pair around
  * its main kernel on the call's stream.  o2mi_kernel_timing_read waits for

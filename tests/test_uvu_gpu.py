@@ -1,0 +1,153 @@
+"""GPU parity of the uvu kernels against the fp64 uvu oracle (gate 1e-5)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import uvu_oracle as U
+from oracle.o2_oracle import normalized_error
+
+TOL = 1e-5
+pytestmark = pytest.mark.gpu
+
+
+def _run(module, x, y, w, g, wrt=(True, True, True)):
+    xt = torch.from_numpy(x).float().cuda().requires_grad_(wrt[0])
+    yt = torch.from_numpy(y).float().cuda().requires_grad_(wrt[1])
+    wt = torch.from_numpy(w).float().cuda().requires_grad_(wrt[2])
+    out = module(xt, yt, wt)
+    inputs = [t for t, want in zip((xt, yt, wt), wrt) if want]
+    grads = torch.autograd.grad(out, inputs, torch.from_numpy(g).float().cuda())
+    torch.cuda.synchronize()
+    return out.detach().double().cpu().numpy(), [t.double().cpu().numpy() for t in grads]
+
+
+def _case(c, v, m, kw, shared, n, seed, wrt=(True, True, True)):
+    from ictc_o2_hp import UvuTensorProduct
+    print(f"uvu case C={c} V={v} M={m} {kw} shared={shared} N={n} wrt={wrt}", flush=True)
+    module = UvuTensorProduct(c, v, m, shared_weights=shared, internal_weights=False, **kw).cuda()
+    plan = U.UvuOraclePlan(c, v, m, **kw)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, plan.width1))
+    y = rng.standard_normal((n, plan.width2))
+    g = rng.standard_normal((n, plan.width1))
+    w = rng.standard_normal((plan.weight_numel,) if shared else (n, plan.weight_numel))
+    w /= np.sqrt(v)
+    out, grads = _run(module, x, y, w, g, wrt)
+    ref_out = U.forward(plan, x, y, w, shared)
+    ref = U.backward(plan, x, y, w, g, shared)
+    assert normalized_error(ref_out, out) <= TOL
+    for r, a in zip([r for r, want in zip(ref, wrt) if want], grads):
+        assert a.shape == r.shape
+        assert normalized_error(r, a) <= TOL
+
+
+CASES = [
+    (64, 1, 4, {"parity": "canonical"}, False, 700),                 # configs[4] TP shape
+    (128, 32, 4, {"parity": "full"}, False, 24),                     # configs[3] shape, few rows
+    (16, 4, 2, {"parity": "full"}, True, 500),                       # shared weights
+    (130, 3, 2, {"parity": "canonical", "parity_in2": "full"}, True, 40),
+    (24, 1, 6, {"parity": "full", "parity_in2": "canonical"}, False, 50),
+    (5, 2, 3, {"parity": "canonical", "m_max_in2": 1, "path_normalization": "path"}, False, 33),
+    (7, 3, 1, {"parity": "full", "normalization": "norm", "path_normalization": "element"},
+     True, 1),
+]
+
+
+@pytest.mark.parametrize("c,v,m,kw,shared,n", CASES)
+def test_uvu_parity(c, v, m, kw, shared, n):
+    _case(c, v, m, kw, shared, n, seed=c * 100 + v * 10 + m)
+
+
+@pytest.mark.parametrize("wrt", [(True, False, False), (False, True, False), (False, False, True),
+                                 (True, False, True)])
+def test_uvu_gradient_roles(wrt):
+    _case(12, 2, 3, {"parity": "full"}, False, 40, seed=5, wrt=wrt)
+    _case(12, 2, 3, {"parity": "full"}, True, 40, seed=6, wrt=wrt)
+
+
+def test_uvu_golden_vectors(golden_uvu):
+    from ictc_o2_hp import UvuTensorProduct
+    cases = {
+        "c3_v2_m2_full": (3, 2, 2, {"parity": "full"}, True),
+        "c4_v1_m4_canonical": (4, 1, 4, {"parity": "canonical"}, False),
+        "c3_v1_m6_full_in2canonical": (3, 1, 6, {"parity": "full", "parity_in2": "canonical"},
+                                       False),
+        "c2_v3_m3_canonical_in2full_m2_path": (2, 3, 3, {"parity": "canonical",
+                                                         "parity_in2": "full", "m_max_in2": 2,
+                                                         "path_normalization": "path"}, False),
+        "c2_v2_m1_full_norm_element": (2, 2, 1, {"parity": "full", "normalization": "norm",
+                                                 "path_normalization": "element"}, True),
+    }
+    for name, (c, v, m, kw, shared) in cases.items():
+        module = UvuTensorProduct(c, v, m, shared_weights=shared, internal_weights=False,
+                                  **kw).cuda()
+        x, y, w, g = (golden_uvu[f"{name}/{k}"] for k in ("x", "y", "w", "g"))
+        out, grads = _run(module, x, y, w, g)
+        for key, value in zip(("out", "dx", "dy", "dw"), [out, *grads]):
+            assert normalized_error(golden_uvu[f"{name}/{key}"], value) <= TOL, (name, key)
+
+
+def test_uvu_empty_rows():
+    from ictc_o2_hp import UvuTensorProduct
+    for shared in (True, False):
+        module = UvuTensorProduct(8, 2, 2, shared_weights=shared, internal_weights=False).cuda()
+        x = torch.zeros(0, module.input1_dimension, device="cuda", requires_grad=True)
+        y = torch.zeros(0, module.input2_dimension, device="cuda", requires_grad=True)
+        w = torch.zeros((module.weight_numel,) if shared else (0, module.weight_numel),
+                        device="cuda", requires_grad=True)
+        out = module(x, y, w)
+        dx, dy, dw = torch.autograd.grad(out, (x, y, w), torch.zeros_like(out))
+        assert out.shape == x.shape and dx.shape == x.shape and dy.shape == y.shape
+        assert dw.shape == w.shape and torch.count_nonzero(dw).item() == 0
+
+
+def test_uvu_into_ops_and_internal_weights():
+    from ictc_o2_hp import UvuTensorProduct, uvu_ops
+    torch.manual_seed(0)
+    module = UvuTensorProduct(16, 1, 4, parity="canonical").cuda()   # internal shared weights
+    x = torch.randn(50, module.input1_dimension, device="cuda")
+    y = torch.randn(50, module.input2_dimension, device="cuda")
+    args = (module._path_info, module._coefficients, module._first_order, module._second_order,
+            module._kernel_metadata_id, True)
+    result = torch.empty_like(x)
+    uvu_ops.uvu_forward_into(x, y, module.weight.detach(), *args, result)
+    assert torch.equal(result, module(x, y))
+    g = torch.randn_like(x)
+    gx, gy, gw = torch.empty_like(x), torch.empty_like(y), torch.empty_like(module.weight)
+    uvu_ops.uvu_backward_into(x, y, module.weight.detach(), g, *args, 7, gx, gy, gw)
+    ref = uvu_ops.uvu_backward(x, y, module.weight.detach(), g, *args, 7)
+    for a, b in zip((gx, gy, gw), ref):
+        assert torch.equal(a, b)
+
+
+def test_uvu_torch_compile():
+    from ictc_o2_hp import UvuTensorProduct
+    torch.manual_seed(1)
+    module = UvuTensorProduct(32, 1, 3, parity="full", shared_weights=False).cuda()
+    compiled = torch.compile(module, fullgraph=True, dynamic=False)
+    x = torch.randn(64, module.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.randn(64, module.input2_dimension, device="cuda", requires_grad=True)
+    w = torch.randn(64, module.weight_numel, device="cuda", requires_grad=True)
+    g = torch.randn_like(x)
+    eager = torch.autograd.grad(module(x, y, w), (x, y, w), g)
+    comp = torch.autograd.grad(compiled(x, y, w), (x, y, w), g)
+    for a, b in zip(eager, comp):
+        assert torch.equal(a, b)
+
+
+def test_uvu_double_backward():
+    from ictc_o2_hp import UvuTensorProduct
+    torch.manual_seed(2)
+    module = UvuTensorProduct(4, 1, 2, parity="full", shared_weights=False).cuda()
+    x = torch.randn(6, module.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.randn(6, module.input2_dimension, device="cuda", requires_grad=True)
+    w = torch.randn(6, module.weight_numel, device="cuda", requires_grad=True)
+    (gy,) = torch.autograd.grad(module(x, y, w).square().sum(), y, create_graph=True)
+    (hw,) = torch.autograd.grad(gy.sum(), w)
+    m64 = UvuTensorProduct(4, 1, 2, parity="full", shared_weights=False).double()
+    x64, y64, w64 = (t.detach().double().cpu().requires_grad_() for t in (x, y, w))
+    (gy64,) = torch.autograd.grad(m64(x64, y64, w64).square().sum(), y64, create_graph=True)
+    (hw64,) = torch.autograd.grad(gy64.sum(), w64)
+    assert normalized_error(hw64.numpy(), hw.double().cpu().numpy()) <= TOL
