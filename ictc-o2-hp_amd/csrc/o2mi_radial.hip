@@ -1,0 +1,232 @@
+// C ABI of the fused radial affine + V=1 uvu product (RadialUvuTensorProduct).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+
+#include "ictc_o2_hp_amd.h"
+#include "o2mi_error.hpp"
+#include "o2mi_radial_launch.hpp"
+
+// Generated registry (radial_registry.hip).
+const o2mi::radial::KernelSet* o2mi_find_radial_set(int m_max, int full, int m_max_in2,
+                                                    int full_in2, int kh);
+
+struct o2mi_radial_plan {
+  const o2mi::radial::KernelSet* set;
+  int C, H;
+  int64_t W1, W2;
+};
+
+namespace o2mi {
+namespace radial {
+namespace {
+
+int fail(int status, const std::string& message) {
+  o2mi_error_slot() = message;
+  return status;
+}
+
+int fail_hip(hipError_t err, const char* where) {
+  o2mi_error_slot() = std::string(where) + ": " + hipGetErrorString(err);
+  return O2MI_ERR_HIP;
+}
+
+// out[c] = sum_s in[s * cols + c] in slice order.
+__global__ __launch_bounds__(256) void slice_sum_kernel(const float* __restrict__ in, int slices,
+                                                        int64_t cols, float* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int k = 0; k < slices; ++k) s += in[(int64_t)k * cols + c];
+  out[c] = s;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = 0.f;
+}
+
+unsigned blocks_for(int64_t items) { return (unsigned)((items + 255) / 256); }
+
+int device_cus() {
+  static std::mutex mu;
+  static int cus[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  int& c = cus[device & 63];
+  if (c == 0) {
+    hipDeviceProp_t prop;
+    c = hipGetDeviceProperties(&prop, device) == hipSuccess ? prop.multiProcessorCount : 256;
+    if (c <= 0) c = 256;
+  }
+  return c;
+}
+
+// Edge slices of the affine-adjoint kernel: about one block per CU, whole
+// staged tiles per slice, no empty slice.
+void slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
+  const int64_t tiles_c = p->C / 16;
+  const int64_t want = std::max<int64_t>(1, (device_cus() + tiles_c - 1) / tiles_c);
+  const int64_t edge_tiles = std::max<int64_t>(1, (n + kWeightEdges - 1) / kWeightEdges);
+  const int64_t s0 = std::min(want, edge_tiles);
+  const int64_t per = ((edge_tiles + s0 - 1) / s0) * kWeightEdges;
+  *per_slice = per;
+  *slices = (int)std::max<int64_t>(1, (n + per - 1) / per);
+}
+
+bool aligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+Args make_args(const o2mi_radial_plan* p, int64_t n, const float* x, const float* y,
+               const float* hidden, const float* alpha, const float* bias, const float* coef) {
+  Args a;
+  a.n = n;
+  a.C = p->C;
+  a.H = p->H;
+  a.W1 = (int)p->W1;
+  a.W2 = (int)p->W2;
+  a.x = x;
+  a.y = y;
+  a.hidden = hidden;
+  a.alpha = alpha;
+  a.bias = bias;
+  a.coef = coef;
+  return a;
+}
+
+int check_inputs(const float* x, const float* y, const float* hidden, const float* alpha,
+                 const float* bias, const float* coef) {
+  if (!x || !y || !hidden || !alpha || !coef)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
+  if (!aligned16(x) || !aligned16(hidden) || !aligned16(alpha))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "x, hidden and alpha must be 16-byte aligned");
+  (void)y;
+  (void)bias;
+  return O2MI_OK;
+}
+
+}  // namespace
+}  // namespace radial
+}  // namespace o2mi
+
+using namespace o2mi::radial;
+
+extern "C" {
+
+int o2mi_radial_plan_create(int channels, int m_max, int parity, int m_max_in2, int parity_in2,
+                            int hidden, o2mi_radial_plan** plan) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  *plan = nullptr;
+  if (channels < 1 || m_max < 0 || m_max_in2 < 0 || hidden < 1 || (parity != 0 && parity != 1) ||
+      (parity_in2 != 0 && parity_in2 != 1))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid radial plan arguments");
+  if (channels % 16 != 0)
+    return fail(O2MI_ERR_UNSUPPORTED, "fused radial kernels need channels % 16 == 0");
+  if (hidden % 4 != 0 || hidden > 64)
+    return fail(O2MI_ERR_UNSUPPORTED, "fused radial kernels need hidden % 4 == 0 and <= 64");
+  const KernelSet* set = o2mi_find_radial_set(m_max, parity, m_max_in2, parity_in2, 16);
+  if (!set)
+    return fail(O2MI_ERR_UNSUPPORTED, "no fused radial kernel compiled for this structure");
+  auto* p = new o2mi_radial_plan;
+  p->set = set;
+  p->C = channels;
+  p->H = hidden;
+  p->W1 = (int64_t)channels * set->comps1;
+  p->W2 = set->comps2;
+  *plan = p;
+  return O2MI_OK;
+}
+
+int o2mi_radial_plan_destroy(o2mi_radial_plan* plan) {
+  delete plan;
+  return O2MI_OK;
+}
+
+int o2mi_radial_paths(const o2mi_radial_plan* plan) { return plan ? plan->set->paths : -1; }
+
+int o2mi_radial_forward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                            const float* hidden, const float* alpha, const float* bias,
+                            const float* coefficients, float* out, int64_t n_rows,
+                            void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (n_rows == 0) return O2MI_OK;
+  if (int st = check_inputs(x, y, hidden, alpha, bias, coefficients)) return st;
+  if (!aligned16(out)) return fail(O2MI_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
+  const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
+  const hipError_t err = plan->set->forward(a, out, static_cast<hipStream_t>(stream));
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial forward launch");
+}
+
+size_t o2mi_radial_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
+                                            int needed) {
+  if (!plan || n_rows <= 0 || !(needed & 24)) return 0;
+  int64_t per = 0;
+  int slices = 0;
+  slicing(plan, n_rows, &per, &slices);
+  const int64_t rows = (int64_t)plan->set->paths * plan->C;
+  return (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
+}
+
+int o2mi_radial_backward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                             const float* hidden, const float* alpha, const float* bias,
+                             const float* coefficients, const float* grad_output, float* gx,
+                             float* gy, float* ghidden, float* galpha, float* gbias,
+                             void* workspace, size_t workspace_bytes, int64_t n_rows, int needed,
+                             void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (needed & ~31) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1..16");
+  if (needed & 16 && !bias)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "bias gradient requested without a bias");
+  if (((needed & 8) && !galpha) || ((needed & 16) && !gbias))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested affine gradient");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows = (int64_t)plan->set->paths * plan->C;
+  if (n_rows == 0) {
+    // No edges: the affine adjoints are zero, the other roles are empty.
+    if (needed & 8) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows * plan->H)), dim3(256),
+                                       0, s, galpha, rows * plan->H);
+    if (needed & 16) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows)), dim3(256), 0, s,
+                                        gbias, rows);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial zero fill");
+  }
+  if (int st = check_inputs(x, y, hidden, alpha, bias, coefficients)) return st;
+  if (!grad_output || !aligned16(grad_output))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "grad_output must be a 16-byte aligned pointer");
+  if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy) ||
+      ((needed & 4) && !aligned16(ghidden)))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
+  if ((needed & 8) && !aligned16(galpha))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "galpha must be 16-byte aligned");
+  const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
+  if (needed & 7) {
+    const hipError_t err = plan->set->backward(a, grad_output, gx, gy, ghidden, needed & 7, s);
+    if (err != hipSuccess) return fail_hip(err, "radial backward launch");
+  }
+  if (needed & 24) {
+    int64_t per = 0;
+    int slices = 0;
+    slicing(plan, n_rows, &per, &slices);
+    const size_t need = (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+      return fail(O2MI_ERR_WORKSPACE,
+                  "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
+    float* part_alpha = static_cast<float*>(workspace);
+    float* part_bias = part_alpha + (int64_t)slices * rows * plan->H;
+    hipError_t err = plan->set->weight(a, grad_output, per, slices, part_alpha, part_bias, s);
+    if (err != hipSuccess) return fail_hip(err, "radial weight launch");
+    if (needed & 8)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows * plan->H)), dim3(256), 0, s,
+                         part_alpha, slices, rows * plan->H, galpha);
+    if (needed & 16)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows)), dim3(256), 0, s, part_bias,
+                         slices, rows, gbias);
+    err = hipGetLastError();
+    if (err != hipSuccess) return fail_hip(err, "radial slice sum launch");
+  }
+  return O2MI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,631 @@
+// Fused radial affine + V=1 O(2) uvu product for gfx950 (CDNA4).
+//
+// RadialUvuTensorProduct (radial_uvu.py:10-66, radial_streamed.py:37-57):
+//   W[e, p*C + u] = sum_h hidden[e, h] alpha[p*C + u, h] + bias[p*C + u]
+//   out[e, k, u, :] += W[e, p*C + u] * CG_p(x[e, i, u, :], y[e, j, :])
+// The affine map runs on the fp32 matrix cores (v_mfma_f32_16x16x4_f32) and
+// each 16-channel x 16-edge weight tile is consumed in registers by the
+// product, so generated weights never reach memory.
+//
+// MFMA 16x16x4 f32 operand layout (checked on gfx950): lane l supplies
+// A[l%16][l/16] and B[l/16][l%16]; D[4*(l/16) + r][l%16] is accumulator r of
+// lane l.  Below, g = lane/16 and j = lane%16.
+//
+// Forward / input adjoints (radial_forward_kernel, radial_backward_kernel).
+// A block of 8 waves owns 128 edges, 16 per wave, and walks the channels in
+// tiles of 16.  Per tile it stages alpha rows p*C + u0 .. +15 of every path
+// (hidden width padded with zeros to 4*KH) and the bias in LDS.  The weight
+// tile is computed as W^T[channel, edge]: A = alpha (lane: row j, h = KH*g+s),
+// B = hidden (lane: edge j, h = KH*g+s), so lane (g, j) ends up holding the
+// weights of edge j for channels u0 + 4g + r, r = 0..3, and loads x, g and
+// writes out / dx for exactly those (edge, channel) pairs.  The hidden
+// adjoint, dh[e, h] = sum_{p,u} gw[e, p, u] alpha[p*C + u, h], reuses the
+// weight adjoint gw in that accumulator layout as the B operand (K index =
+// channel 4g + s at step s) against alpha read transposed from LDS.
+//
+// Affine-parameter adjoints (radial_weight_kernel).  dalpha = gw^T hidden and
+// dbias = sum_e gw are sums over all edges.  A block owns one channel tile and
+// a contiguous slice of edges; each wave owns the paths p = wave (mod 8) and
+// keeps their dalpha tiles in accumulators for the whole slice.  Per 32 edges
+// the block stages x, g (the tile's channels), y and hidden in LDS (double
+// buffered, next tile prefetched into registers during compute); lane (g, j)
+// forms gw for channel u0 + j and edge 4s + g at step s, which is the B
+// operand of dalpha^T[h, channel] += hidden^T[h, edge] gw[edge, channel].
+// Slice partials are summed in a fixed order afterwards: no atomics, the
+// result is bitwise reproducible for a given edge count and device.
+//
+// Coupling values come from the module's fp32 [P][2][2][2] buffer at run time
+// (any normalisation); which of the 8 slots are non-zero is fixed by the plan.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace o2mi {
+namespace radial {
+
+struct REntry {
+  int off;   // first input: offset in units of C; second input (V = 1): absolute offset
+  int dim;   // 1 or 2
+  int base;  // first input: component index within one (edge, channel); second: within the row
+};
+
+struct RPath {
+  int i, j, k;
+  int mask;  // bit (c*4 + a*2 + b): coupling slot [out c][in1 a][in2 b] is non-zero
+};
+
+using f4 = float __attribute__((ext_vector_type(4)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kEdgesPerWave = 16;
+constexpr int kEdgesPerBlock = kEdgesPerWave * kWaves;
+constexpr int kWeightEdges = 32;  // edges per staged tile of the affine-adjoint kernel
+constexpr uint32_t kIdle = 0x80000000u;
+constexpr int kRsrcFlags = 0x00020000;
+
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+template <int KH>
+struct Geom {
+  static constexpr int kHid = 4 * KH;      // padded hidden width
+  static constexpr int kRow = kHid + 4;    // LDS row stride of the alpha tile (floats)
+  static constexpr int kTiles = kHid / 16; // 16-row tiles of the hidden / alpha adjoints
+  static_assert(KH % 4 == 0, "KH must be a multiple of 4");
+};
+
+// LDS of the forward / input-adjoint kernels, one array: couplings and bias
+// first, so that their uniform or lane-base addresses reach every path with a
+// 16-bit immediate offset, then the alpha tile.
+template <int P, int KH>
+struct ALayout {
+  static constexpr int kCoef = 0;
+  static constexpr int kBias = P * 8;
+  static constexpr int kAlpha = P * 24;
+  static constexpr int kFloats = kAlpha + P * 16 * Geom<KH>::kRow;
+  static_assert(kAlpha % 4 == 0, "alpha tile must be 16-byte aligned");
+};
+
+struct Args {
+  int64_t n;  // edges
+  int C;      // channels (multiple of 16)
+  int H;      // hidden width (multiple of 4, <= 4*KH)
+  int W1;     // C * components of the first input
+  int W2;     // width of the second input
+  const float* x;
+  const float* y;
+  const float* hidden;
+  const float* alpha;  // [P*C, H]
+  const float* bias;   // [P*C] or null
+  const float* coef;   // [P][2][2][2]
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int64_t row0,
+                                                            int width, int64_t rows) {
+  const int64_t valid = rows < 0 ? 0 : rows;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base) + row0 * width, 0,
+                                           (int)(valid * width * 4), kRsrcFlags);
+}
+
+__device__ __forceinline__ float ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0));
+}
+
+__device__ __forceinline__ f4 ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));
+}
+
+__device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, f4 v, uint32_t voff) {
+  // Non-temporal: outputs are not read again by this kernel.
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)voff, 0, 2);
+}
+
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Stage alpha rows p*C + u0 + r (r < 16) of every path, zero-padded to the
+// padded hidden width, and the matching bias entries.
+template <int P, int KH>
+__device__ __forceinline__ void stage_alpha(float* s_mem, const Args& a, int u0) {
+  using G = Geom<KH>;
+  using L = ALayout<P, KH>;
+  float* s_alpha = s_mem + L::kAlpha;
+  float* s_bias = s_mem + L::kBias;
+  constexpr int kVec = G::kHid / 4;
+  for (int idx = threadIdx.x; idx < P * 16 * kVec; idx += kThreads) {
+    const int q = idx % kVec;
+    const int pr = idx / kVec;  // p * 16 + r
+    const int p = pr >> 4, r = pr & 15;
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (4 * q < a.H)
+      v = *reinterpret_cast<const f4*>(a.alpha + (int64_t)(p * a.C + u0 + r) * a.H + 4 * q);
+    *reinterpret_cast<f4*>(s_alpha + pr * G::kRow + 4 * q) = v;
+  }
+  for (int idx = threadIdx.x; idx < P * 16; idx += kThreads)
+    s_bias[idx] = a.bias ? a.bias[(idx >> 4) * a.C + u0 + (idx & 15)] : 0.f;
+}
+
+// The 4 x dim values of one first-input entry for channels u .. u+3 of one row.
+template <int Dim>
+__device__ __forceinline__ void load_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int off_c,
+                                           int u, float* dst) {
+  const uint32_t voff = row_off + (uint32_t)(off_c + Dim * u) * 4u;
+  const f4 v0 = ld4(r, voff);
+  dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
+  if constexpr (Dim == 2) {
+    const f4 v1 = ld4(r, voff + 16u);
+    dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+  }
+}
+
+template <int Dim>
+__device__ __forceinline__ void store_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int off_c,
+                                            int u, const float* src) {
+  const uint32_t voff = row_off + (uint32_t)(off_c + Dim * u) * 4u;
+  st4(r, f4{src[0], src[1], src[2], src[3]}, voff);
+  if constexpr (Dim == 2) st4(r, f4{src[4], src[5], src[6], src[7]}, voff + 16u);
+}
+
+template <class Plan>
+__device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int C, int u,
+                                         float* v) {
+  static_for<Plan::kEntries1>([&](auto ec) {
+    constexpr REntry e = Plan::e1[decltype(ec)::value];
+    load_entry<e.dim>(r, row_off, e.off * C, u, v + 4 * e.base);
+  });
+}
+
+template <class Plan>
+__device__ __forceinline__ void store_row(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int C,
+                                          int u, const float* v) {
+  static_for<Plan::kEntries1>([&](auto ec) {
+    constexpr REntry e = Plan::e1[decltype(ec)::value];
+    store_entry<e.dim>(r, row_off, e.off * C, u, v + 4 * e.base);
+  });
+}
+
+// hidden[edge j][KH*g + s], zero past the hidden width.
+template <int KH>
+__device__ __forceinline__ void load_hidden(__amdgpu_buffer_rsrc_t rh, int H, int g, int j,
+                                            float* hid) {
+  static_for<KH / 4>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const int h = KH * g + 4 * q;
+    const uint32_t voff = h < H ? (uint32_t)(j * H + h) * 4u : kIdle;
+    const f4 v = ld4(rh, voff);
+    hid[4 * q] = v.x; hid[4 * q + 1] = v.y; hid[4 * q + 2] = v.z; hid[4 * q + 3] = v.w;
+  });
+}
+
+// W^T tile of path p: bias + sum_h alpha[p*C + u0 + 4g + r, h] hidden[j, h].
+// bias_off = kBias + 4g and arow_off = kAlpha + j*kRow + KH*g are the lane's
+// base offsets (laundered once per channel tile by the caller).
+template <int KH>
+__device__ __forceinline__ f4 weight_tile(const float* s_mem, int bias_off, int arow_off, int p,
+                                          const float* hid) {
+  using G = Geom<KH>;
+  f4 w = *reinterpret_cast<const f4*>(s_mem + bias_off + p * 16);
+  const float* arow = s_mem + arow_off + p * 16 * G::kRow;
+  static_for<KH / 4>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const f4 av = *reinterpret_cast<const f4*>(arow + 4 * q);
+    w = mfma(av.x, hid[4 * q], w);
+    w = mfma(av.y, hid[4 * q + 1], w);
+    w = mfma(av.z, hid[4 * q + 2], w);
+    w = mfma(av.w, hid[4 * q + 3], w);
+  });
+  return w;
+}
+
+template <class Plan, int KH>
+__global__ __launch_bounds__(kThreads, 1) void radial_forward_kernel(Args a, float* out) {
+  using G = Geom<KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int NC = Plan::kComps1;
+  using L = ALayout<P, KH>;
+  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
+  float* s_coef = s_mem + L::kCoef;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
+  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
+  const auto rx = rows_rsrc(a.x, e0, a.W1, rows);
+  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
+  const auto ro = rows_rsrc(out, e0, a.W1, rows);
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
+  float hid[KH];
+  load_hidden<KH>(rh, a.H, g, j, hid);
+  float yv[Plan::kComps2];
+  static_for<Plan::kComps2>([&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
+  });
+
+  for (int u0 = 0; u0 < a.C; u0 += 16) {
+    __syncthreads();
+    stage_alpha<P, KH>(s_mem, a, u0);
+    __syncthreads();
+    const int u = u0 + 4 * g;
+    // Laundered per tile so that neither addresses nor the uniform coupling
+    // reads are hoisted out of the channel loop into registers.
+    int coef_off = L::kCoef, bias_off = L::kBias + 4 * g;
+    int arow_off = L::kAlpha + j * G::kRow + KH * g;
+    asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off));
+    const float* cf_tile = s_mem + coef_off;
+    float xv[4 * NC];
+    load_row<Plan>(rx, xrow, a.C, u, xv);
+    float ov[4 * NC];
+    static_for<4 * NC>([&](auto ic) { ov[decltype(ic)::value] = 0.f; });
+    static_for<P>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr RPath ps = Plan::paths[p];
+      constexpr REntry X = Plan::e1[ps.i];
+      constexpr REntry Y = Plan::e2[ps.j];
+      constexpr REntry O = Plan::e1[ps.k];
+      const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, p, hid);
+      static_for<8>([&](auto sc) {
+        constexpr int slot = decltype(sc)::value;
+        constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
+        if constexpr ((ps.mask >> slot) & 1) {
+          const float cy = cf_tile[p * 8 + slot] * yv[Y.base + ib];
+          static_for<4>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            ov[4 * O.base + r * O.dim + c] += cy * (xv[4 * X.base + r * X.dim + ia] * w[r]);
+          });
+        }
+      });
+      // Keep each path's LDS reads and MFMAs together: interleaving the
+      // unrolled paths costs registers, not time (two waves per SIMD).
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    store_row<Plan>(ro, xrow, a.C, u, ov);
+  }
+}
+
+// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here).
+template <class Plan, int KH>
+__global__ __launch_bounds__(kThreads, 1) void radial_backward_kernel(Args a, const float* gout,
+                                                                       float* gx, float* gy,
+                                                                       float* ghid, int needed) {
+  using G = Geom<KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int NC = Plan::kComps1;
+  constexpr int NY = Plan::kComps2;
+  using L = ALayout<P, KH>;
+  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
+  float* s_coef = s_mem + L::kCoef;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
+  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
+  const auto rx = rows_rsrc(a.x, e0, a.W1, rows);
+  const auto rg = rows_rsrc(gout, e0, a.W1, rows);
+  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;
+  // Every role is computed; a role that is not requested gets a zero-size
+  // store descriptor.  Branches on the roles cost more registers (the
+  // compiler duplicates the channel loop) than the rarely skipped work.
+  const bool need_y = (needed & 2) != 0;
+  const auto rdx = rows_rsrc(gx, e0, a.W1, (needed & 1) ? rows : 0);
+  const auto rgh = rows_rsrc(ghid, e0, a.H, (needed & 4) ? rows : 0);
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
+  float hid[KH];
+  load_hidden<KH>(rh, a.H, g, j, hid);
+  float yv[NY], dyv[NY];
+  static_for<NY>([&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
+    dyv[c] = 0.f;
+  });
+  f4 gh[G::kTiles];
+  static_for<G::kTiles>([&](auto tc) { gh[decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
+
+  for (int u0 = 0; u0 < a.C; u0 += 16) {
+    __syncthreads();
+    stage_alpha<P, KH>(s_mem, a, u0);
+    __syncthreads();
+    const int u = u0 + 4 * g;
+    int coef_off = L::kCoef, bias_off = L::kBias + 4 * g;
+    int arow_off = L::kAlpha + j * G::kRow + KH * g, acol_off = L::kAlpha + 4 * g * G::kRow + j;
+    asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off));
+    const float* cf_tile = s_mem + coef_off;
+    float xv[4 * NC], gv[4 * NC], dxv[4 * NC];
+    load_row<Plan>(rx, xrow, a.C, u, xv);
+    load_row<Plan>(rg, xrow, a.C, u, gv);
+    static_for<4 * NC>([&](auto ic) { dxv[decltype(ic)::value] = 0.f; });
+    static_for<P>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr RPath ps = Plan::paths[p];
+      constexpr REntry X = Plan::e1[ps.i];
+      constexpr REntry Y = Plan::e2[ps.j];
+      constexpr REntry O = Plan::e1[ps.k];
+      const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, p, hid);
+      float gw[4] = {0.f, 0.f, 0.f, 0.f};
+      static_for<8>([&](auto sc) {
+        constexpr int slot = decltype(sc)::value;
+        constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
+        if constexpr ((ps.mask >> slot) & 1) {
+          const float cf = cf_tile[p * 8 + slot];
+          const float cy = cf * yv[Y.base + ib];
+          static_for<4>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            const float xr = xv[4 * X.base + r * X.dim + ia];
+            const float gr = gv[4 * O.base + r * O.dim + c];
+            gw[r] += cy * (xr * gr);
+            dyv[Y.base + ib] += cf * (xr * gr) * w[r];
+            dxv[4 * X.base + r * X.dim + ia] += cy * (gr * w[r]);
+          });
+        }
+      });
+      const float* acol = s_mem + acol_off + p * 16 * G::kRow;
+      static_for<G::kTiles>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        gh[t] = mfma(acol[16 * t], gw[0], gh[t]);
+        gh[t] = mfma(acol[G::kRow + 16 * t], gw[1], gh[t]);
+        gh[t] = mfma(acol[2 * G::kRow + 16 * t], gw[2], gh[t]);
+        gh[t] = mfma(acol[3 * G::kRow + 16 * t], gw[3], gh[t]);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    store_row<Plan>(rdx, xrow, a.C, u, dxv);
+  }
+  if (need_y) {
+    // Lanes j, j+16, j+32, j+48 hold the channel partial sums of edge j.
+    static_for<NY>([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      dyv[c] += __shfl_xor(dyv[c], 16);
+      dyv[c] += __shfl_xor(dyv[c], 32);
+    });
+    if (g == 0 && j < rows) {
+      float* dst = gy + (e0 + j) * a.W2;
+      static_for<NY>([&](auto cc) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
+    }
+  }
+  static_for<G::kTiles>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    const int h = 16 * t + 4 * g;
+    st4(rgh, gh[t], h < a.H ? (uint32_t)(j * a.H + h) * 4u : kIdle);
+  });
+}
+
+// Staged tile of the affine-adjoint kernel: kWeightEdges edges of x and g
+// (this block's 16 channels), y and hidden.  Row strides are odd / 16 mod 32
+// so the per-step LDS reads of 4 edges x 16 channels do not collide in banks.
+template <class Plan, int KH>
+struct WTile {
+  static constexpr int kXS = 16 * Plan::kComps1 + 1;
+  static constexpr int kYS = Plan::kComps2;
+  static constexpr int kHS = Geom<KH>::kHid + 16;
+  static constexpr int kX = kWeightEdges * kXS;
+  static constexpr int kY = kWeightEdges * kYS;
+  static constexpr int kH = kWeightEdges * kHS;
+  static constexpr int kFloats = 2 * kX + kY + kH;
+  // Per-thread staging registers: ceil(elements / threads) per part.
+  static constexpr int kXPer = (kWeightEdges * 16 * Plan::kComps1 + kThreads - 1) / kThreads;
+  static constexpr int kYPer = (kY + kThreads - 1) / kThreads;
+  static constexpr int kHPer = (kWeightEdges * Geom<KH>::kHid + kThreads - 1) / kThreads;
+};
+
+template <class Plan, int KH>
+struct WPrefetch {
+  float x[WTile<Plan, KH>::kXPer], g[WTile<Plan, KH>::kXPer];
+  float y[WTile<Plan, KH>::kYPer], h[WTile<Plan, KH>::kHPer];
+};
+
+// Element idx of the x/g part of a tile: edge idx / (16 NC), then the
+// channel-tile component (entry-major, [channel][component] inside an entry).
+template <class Plan>
+__device__ __forceinline__ int tile_x_offset(int idx_in_edge, int C, int u0) {
+  int off = 0;
+  static_for<Plan::kEntries1>([&](auto ec) {
+    constexpr REntry e = Plan::e1[decltype(ec)::value];
+    const int lo = 16 * e.base, hi = 16 * (e.base + e.dim);
+    if (idx_in_edge >= lo && idx_in_edge < hi) off = e.off * C + e.dim * u0 + (idx_in_edge - lo);
+  });
+  return off;
+}
+
+template <class Plan, int KH>
+__device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH>& pf, const Args& a,
+                                             const float* gout, int64_t t0, int64_t t_end,
+                                             int u0) {
+  using T = WTile<Plan, KH>;
+  constexpr int XE = 16 * Plan::kComps1;
+  const int64_t rows = t_end - t0 < kWeightEdges ? t_end - t0 : kWeightEdges;
+  const auto rx = rows_rsrc(a.x, t0, a.W1, rows);
+  const auto rg = rows_rsrc(gout, t0, a.W1, rows);
+  const auto ry = rows_rsrc(a.y, t0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, t0, a.H, rows);
+  static_for<T::kXPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    uint32_t voff = kIdle;
+    if (idx < kWeightEdges * XE) {
+      const int edge = idx / XE;
+      voff = (uint32_t)(edge * a.W1 + tile_x_offset<Plan>(idx - edge * XE, a.C, u0)) * 4u;
+    }
+    pf.x[k] = ld1(rx, voff);
+    pf.g[k] = ld1(rg, voff);
+  });
+  static_for<T::kYPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    pf.y[k] = ld1(ry, idx < T::kY ? (uint32_t)idx * 4u : kIdle);  // rows of y are contiguous
+  });
+  static_for<T::kHPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    const int edge = idx / Geom<KH>::kHid, h = idx - edge * Geom<KH>::kHid;
+    const bool ok = idx < kWeightEdges * Geom<KH>::kHid && h < a.H;
+    pf.h[k] = ld1(rh, ok ? (uint32_t)(edge * a.H + h) * 4u : kIdle);
+  });
+}
+
+template <class Plan, int KH>
+__device__ __forceinline__ void weight_commit(const WPrefetch<Plan, KH>& pf, float* buf) {
+  using T = WTile<Plan, KH>;
+  constexpr int XE = 16 * Plan::kComps1;
+  float* sx = buf;
+  float* sg = buf + T::kX;
+  float* sy = buf + 2 * T::kX;
+  float* sh = sy + T::kY;
+  static_for<T::kXPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    if (idx < kWeightEdges * XE) {
+      const int edge = idx / XE, rest = idx - edge * XE;
+      sx[edge * T::kXS + rest] = pf.x[k];
+      sg[edge * T::kXS + rest] = pf.g[k];
+    }
+  });
+  static_for<T::kYPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    if (idx < T::kY) sy[idx] = pf.y[k];
+  });
+  static_for<T::kHPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * kThreads;
+    if (idx < kWeightEdges * Geom<KH>::kHid) {
+      const int edge = idx / Geom<KH>::kHid, h = idx - edge * Geom<KH>::kHid;
+      sh[edge * T::kHS + h] = pf.h[k];
+    }
+  });
+}
+
+// Grid (slices, C/16).  part_alpha: [slices][P*C][H]; part_bias: [slices][P*C].
+template <class Plan, int KH>
+__global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
+    Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
+  using G = Geom<KH>;
+  using T = WTile<Plan, KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int NPW = (P + kWaves - 1) / kWaves;
+  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
+  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
+  float* s_coef = s_mem;
+  float* s_tile = s_mem + kCoefPad;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int u0 = blockIdx.y * 16;
+  const int64_t begin = (int64_t)blockIdx.x * edges_per_slice;
+  const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
+  const int tiles = end > begin ? (int)((end - begin + kWeightEdges - 1) / kWeightEdges) : 0;
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
+  f4 ga[NPW][G::kTiles];
+  float gb[NPW];
+  static_for<NPW>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    gb[q] = 0.f;
+    static_for<G::kTiles>([&](auto tc) { ga[q][decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
+  });
+
+  WPrefetch<Plan, KH> pf;
+  if (tiles > 0) {
+    weight_fetch<Plan, KH>(pf, a, gout, begin, end, u0);
+    weight_commit<Plan, KH>(pf, s_tile);
+  }
+  __syncthreads();
+  for (int t = 0; t < tiles; ++t) {
+    const bool more = t + 1 < tiles;
+    if (more) weight_fetch<Plan, KH>(pf, a, gout, begin + (int64_t)(t + 1) * kWeightEdges, end, u0);
+    const float* buf = s_tile + (t & 1) * T::kFloats;
+    const float* sx = buf;
+    const float* sg = buf + T::kX;
+    const float* sy = buf + 2 * T::kX;
+    const float* sh = sy + T::kY;
+#pragma unroll 1
+    for (int s = 0; s < kWeightEdges / 4; ++s) {
+      const int edge = 4 * s + g;
+      int coef_off = 0;
+      asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
+      const float* cf_step = s_coef + coef_off;
+      float xv[Plan::kComps1], gv[Plan::kComps1], yv[Plan::kComps2], hv[G::kTiles];
+      static_for<Plan::kEntries1>([&](auto ec) {
+        constexpr REntry e = Plan::e1[decltype(ec)::value];
+        static_for<e.dim>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          const int o = edge * T::kXS + 16 * e.base + j * e.dim + d;
+          xv[e.base + d] = sx[o];
+          gv[e.base + d] = sg[o];
+        });
+      });
+      static_for<Plan::kComps2>([&](auto cc) {
+        yv[decltype(cc)::value] = sy[edge * T::kYS + decltype(cc)::value];
+      });
+      static_for<G::kTiles>([&](auto tc) {
+        hv[decltype(tc)::value] = sh[edge * T::kHS + 16 * decltype(tc)::value + j];
+      });
+      static_for<P>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        constexpr int q = p / kWaves;
+        if (wave == p % kWaves) {
+          constexpr RPath ps = Plan::paths[p];
+          constexpr REntry X = Plan::e1[ps.i];
+          constexpr REntry Y = Plan::e2[ps.j];
+          constexpr REntry O = Plan::e1[ps.k];
+          float gw = 0.f;
+          static_for<8>([&](auto sc) {
+            constexpr int slot = decltype(sc)::value;
+            constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
+            if constexpr ((ps.mask >> slot) & 1)
+              gw += cf_step[p * 8 + slot] * yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+          });
+          gb[q] += gw;
+          static_for<G::kTiles>([&](auto tc) {
+            constexpr int tt = decltype(tc)::value;
+            ga[q][tt] = mfma(hv[tt], gw, ga[q][tt]);
+          });
+        }
+      });
+    }
+    if (more) weight_commit<Plan, KH>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
+    __syncthreads();
+  }
+
+  const int64_t PC = (int64_t)P * a.C;
+  float* pa = part_alpha + (int64_t)blockIdx.x * PC * a.H;
+  float* pb = part_bias + (int64_t)blockIdx.x * PC;
+  static_for<P>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int q = p / kWaves;
+    if (wave == p % kWaves) {
+      const int64_t row = (int64_t)p * a.C + u0 + j;
+      static_for<G::kTiles>([&](auto tc) {
+        constexpr int tt = decltype(tc)::value;
+        const int h = 16 * tt + 4 * g;
+        if (h < a.H) *reinterpret_cast<f4*>(pa + row * a.H + h) = ga[q][tt];
+      });
+      float b = gb[q];
+      b += __shfl_xor(b, 16);
+      b += __shfl_xor(b, 32);
+      if (g == 0) pb[row] = b;
+    }
+  });
+}
+
+}  // namespace radial
+}  // namespace o2mi

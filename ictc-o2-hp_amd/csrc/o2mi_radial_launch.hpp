@@ -1,0 +1,64 @@
+// Host launchers of the fused radial kernels, one kernel set per plan.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "o2mi_radial.hpp"
+
+namespace o2mi {
+namespace radial {
+
+struct KernelSet {
+  int paths;
+  int comps1;   // components per channel of the first input
+  int comps2;   // width of the second input (V = 1)
+  int kh;       // hidden width supported: <= 4 * kh
+  hipError_t (*forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, float* ghid,
+                         int needed, hipStream_t);
+  hipError_t (*weight)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
+                       float* part_alpha, float* part_bias, hipStream_t);
+};
+
+inline unsigned edge_blocks(int64_t n) {
+  return (unsigned)((n + kEdgesPerBlock - 1) / kEdgesPerBlock);
+}
+
+template <class Plan, int KH>
+hipError_t launch_forward(const Args& a, float* out, hipStream_t s) {
+  hipLaunchKernelGGL((radial_forward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads), 0,
+                     s, a, out);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* gy, float* ghid,
+                           int needed, hipStream_t s) {
+  hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads),
+                     0, s, a, gout, gx, gy, ghid, needed);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_slice, int slices,
+                         float* part_alpha, float* part_bias, hipStream_t s) {
+  hipLaunchKernelGGL((radial_weight_kernel<Plan, KH>), dim3((unsigned)slices, (unsigned)(a.C / 16)),
+                     dim3(kThreads), 0, s, a, gout, edges_per_slice, part_alpha, part_bias);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+const KernelSet* kernel_set() {
+  static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
+                                &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
+                                &launch_weight<Plan, KH>};
+  return &set;
+}
+
+}  // namespace radial
+}  // namespace o2mi
+
+#define O2MI_DEFINE_RADIAL_SET(NAME, KH)                                     \
+  const o2mi::radial::KernelSet* o2mi_radial_set_##NAME##_##KH() {           \
+    return o2mi::radial::kernel_set<o2mi::radial::plans::NAME, KH>();        \
+  }

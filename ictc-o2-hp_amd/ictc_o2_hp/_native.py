@@ -70,6 +70,20 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_uvu_backward_workspace_bytes.argtypes = [prob, c_int]
     lib.o2mi_uvu_backward_f32.restype = c_int
     lib.o2mi_uvu_backward_f32.argtypes = [prob, fp, fp, fp, fp, fp, fp, fp, c_int, vp, c_sz, vp]
+    lib.o2mi_radial_plan_create.restype = c_int
+    lib.o2mi_radial_plan_create.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int,
+                                            ctypes.POINTER(vp)]
+    lib.o2mi_radial_plan_destroy.restype = c_int
+    lib.o2mi_radial_plan_destroy.argtypes = [vp]
+    lib.o2mi_radial_paths.restype = c_int
+    lib.o2mi_radial_paths.argtypes = [vp]
+    lib.o2mi_radial_forward_f32.restype = c_int
+    lib.o2mi_radial_forward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, c_i64, vp]
+    lib.o2mi_radial_backward_workspace_bytes.restype = c_sz
+    lib.o2mi_radial_backward_workspace_bytes.argtypes = [vp, c_i64, c_int]
+    lib.o2mi_radial_backward_f32.restype = c_int
+    lib.o2mi_radial_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp,
+                                             vp, c_sz, c_i64, c_int, vp]
     lib.o2mi_tp_launch_shape.restype = c_int
     lib.o2mi_tp_launch_shape.argtypes = [vp, c_i64, c_int] + [ctypes.POINTER(c_int)] * 4
     lib.o2mi_kernel_timing.restype = c_int

@@ -132,6 +132,50 @@ int o2mi_uvu_backward_f32(const o2mi_uvu_problem *problem, const float *x, const
                           const float *w, const float *g, float *gx, float *gy, float *gw,
                           int needed, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- radial affine fused with a V=1 uvu product (RadialUvuTensorProduct) --
+ * out = uvu(x, y; W) with per-edge weights W = hidden @ alpha^T + bias
+ * generated inside the kernel (radial_uvu.py:10-66, radial_streamed.py:37-57).
+ * Layouts: x, out, g, dx [N, C*K1] as the uvu first input ([copy, channel,
+ * component] entries); y, dy [N, K2] (V = 1); hidden, dhidden [N, H];
+ * alpha, dalpha [P*C, H] (torch.nn.Linear.weight); bias, dbias [P*C];
+ * coefficients [P][2][2][2] (the tp module's _coefficients).  x, out, g, dx,
+ * hidden, dhidden, alpha, dalpha and the workspace must be 16-byte aligned. */
+typedef struct o2mi_radial_plan o2mi_radial_plan;
+
+/* Plan for a uvu structure (m_max, parity, m_max_in2, parity_in2), C channels
+ * and hidden width H.  O2MI_ERR_UNSUPPORTED when no fused kernel exists for
+ * it (C % 16 != 0, H % 4 != 0, H > 64, or a structure whose alpha tile does
+ * not fit in LDS); callers then compose the affine map and the uvu product.
+ * Replaces the block policy of radial_streamed.py:17-34. */
+int o2mi_radial_plan_create(int channels, int m_max, int parity, int m_max_in2,
+                            int parity_in2, int hidden, o2mi_radial_plan **plan);
+int o2mi_radial_plan_destroy(o2mi_radial_plan *plan);
+
+/* Number of paths P of the plan's structure. */
+int o2mi_radial_paths(const o2mi_radial_plan *plan);
+
+/* out = tp(x, y, hidden @ alpha^T + bias); bias may be NULL.  Replaces the
+ * radial_stream_forward op (radial_streamed.py:81-99). */
+int o2mi_radial_forward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                            const float *hidden, const float *alpha, const float *bias,
+                            const float *coefficients, float *out, int64_t n_rows,
+                            void *stream);
+
+/* Workspace of o2mi_radial_backward_f32 (non-zero when dalpha or dbias is
+ * requested). */
+size_t o2mi_radial_backward_workspace_bytes(const o2mi_radial_plan *plan, int64_t n_rows,
+                                            int needed);
+
+/* Adjoints at cotangent g for the roles in `needed`: 1 x, 2 y, 4 hidden,
+ * 8 alpha, 16 bias (the mask of radial_streamed.py:109-139).  dalpha and dbias
+ * are fixed-order fp32 sums over edges; n_rows == 0 writes them as zero. */
+int o2mi_radial_backward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                             const float *hidden, const float *alpha, const float *bias,
+                             const float *coefficients, const float *grad_output, float *dx,
+                             float *dy, float *dhidden, float *dalpha, float *dbias,
+                             void *workspace, size_t workspace_bytes, int64_t n_rows,
+                             int needed, void *stream);
+
 /* Kernel timing for measurement harnesses (no counterpart in the reference):
  * while enabled, every forward/backward call records a HIP event pair around
  * its main kernel on the call's stream.  o2mi_kernel_timing_read waits for

@@ -1,0 +1,135 @@
+"""CPU checks of RadialUvuTensorProduct: construction contract, the composed
+path against the radial oracle, and the fused-structure table."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import uvu_oracle as U
+from oracle.o2_oracle import normalized_error
+
+
+def _modules(c=4, m=2, parity="canonical", parity_in2=None, hidden=8, bias=True, **kw):
+    from ictc_o2_hp import RadialUvuTensorProduct, UvuTensorProduct
+    tp = UvuTensorProduct(c, 1, m, parity=parity, parity_in2=parity_in2, shared_weights=False,
+                          **kw)
+    linear = torch.nn.Linear(hidden, tp.weight_numel, bias=bias)
+    return tp, linear, RadialUvuTensorProduct(tp, linear)
+
+
+def test_constructor_contract():
+    from ictc_o2_hp import RadialUvuTensorProduct, UvuTensorProduct
+    tp = UvuTensorProduct(4, 1, 2, shared_weights=False)
+    with pytest.raises(TypeError):
+        RadialUvuTensorProduct(torch.nn.Linear(2, 2), torch.nn.Linear(2, tp.weight_numel))
+    with pytest.raises(ValueError):
+        RadialUvuTensorProduct(UvuTensorProduct(4, 2, 2, shared_weights=False),
+                               torch.nn.Linear(3, 4 * 2 * 10))
+    with pytest.raises(ValueError):
+        RadialUvuTensorProduct(UvuTensorProduct(4, 1, 2), torch.nn.Linear(3, tp.weight_numel))
+    with pytest.raises(TypeError):
+        RadialUvuTensorProduct(tp, torch.nn.Sequential(torch.nn.Linear(3, tp.weight_numel)))
+    with pytest.raises(ValueError):
+        RadialUvuTensorProduct(tp, torch.nn.Linear(3, tp.weight_numel + 1))
+    module = RadialUvuTensorProduct(tp, torch.nn.Linear(3, tp.weight_numel))
+    # External-weight TPs keep an empty persistent "weight" buffer (uvu_o2.py:156).
+    assert sorted(module.state_dict()) == ["radial_out.bias", "radial_out.weight", "tp.weight"]
+    assert module.tp is tp
+
+
+def test_forward_validation():
+    tp, linear, module = _modules()
+    x = torch.randn(5, tp.input1_dimension)
+    y = torch.randn(5, tp.input2_dimension)
+    h = torch.randn(5, 8)
+    with pytest.raises(ValueError):
+        module(x[:, :-1], y, h)
+    with pytest.raises(ValueError):
+        module(x, y[:4], h)
+    with pytest.raises(ValueError):
+        module(x, y, h[:, :-1])
+    with pytest.raises(TypeError):
+        module(x.long(), y.long(), h.long())
+    with pytest.raises(ValueError):
+        module(x.double(), y, h)
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_composed_path_matches_oracle(bias):
+    tp, linear, module = _modules(c=3, m=3, parity="full", parity_in2="canonical", hidden=5,
+                                  bias=bias, path_normalization="path")
+    module = module.double()
+    plan = U.UvuOraclePlan(3, 1, 3, parity="full", parity_in2="canonical",
+                           path_normalization="path")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((7, plan.width1))
+    y = rng.standard_normal((7, plan.width2))
+    h = rng.standard_normal((7, 5))
+    g = rng.standard_normal((7, plan.width1))
+    xt, yt, ht = (torch.from_numpy(a).requires_grad_() for a in (x, y, h))
+    out = module(xt, yt, ht)
+    params = [linear.weight] + ([linear.bias] if bias else [])
+    grads = torch.autograd.grad(out, [xt, yt, ht, *params], torch.from_numpy(g))
+    alpha = linear.weight.detach().numpy()
+    b = linear.bias.detach().numpy() if bias else None
+    ref_out = U.radial_forward(plan, x, y, h, alpha, b)
+    ref = U.radial_backward(plan, x, y, h, alpha, b, g)
+    assert normalized_error(ref_out, out.detach().numpy()) <= 1e-12
+    for r, a in zip([v for v in ref if v is not None], grads):
+        assert normalized_error(r, a.numpy()) <= 1e-12
+
+
+def test_batch_shapes_on_cpu():
+    tp, linear, module = _modules()
+    x = torch.randn(2, 3, tp.input1_dimension)
+    y = torch.randn(2, 3, tp.input2_dimension)
+    h = torch.randn(2, 3, 8)
+    out = module(x, y, h)
+    assert out.shape == x.shape
+    flat = module(x.reshape(6, -1), y.reshape(6, -1), h.reshape(6, -1))
+    assert torch.allclose(out.reshape(6, -1), flat)
+
+
+def test_fused_structure_table():
+    """The fused kernels cover the structures whose alpha tile fits in LDS."""
+    import build_native
+    from ictc_o2_hp.uvu_o2 import ReferenceUvuTensorProduct
+    names = {build_native._radial_name(*s) for s in build_native.RADIAL_STRUCTURES}
+    assert "R4c4c" in names                      # configs[4]: C64, m4, canonical
+    for m, parity, m2, parity2 in build_native.RADIAL_STRUCTURES:
+        tp = ReferenceUvuTensorProduct(16, 1, m, parity=parity, m_max_in2=m2,
+                                       parity_in2=parity2, shared_weights=False)
+        assert 4 * len(tp.paths) * (24 + 16 * 68) <= 160 * 1024
+
+
+def test_library_exports_radial_symbols():
+    from ictc_o2_hp import _native
+    try:
+        lib = _native.library()
+    except _native.NativeLibraryError:
+        pytest.skip("library not built")
+    for name in ("o2mi_radial_plan_create", "o2mi_radial_plan_destroy", "o2mi_radial_paths",
+                 "o2mi_radial_forward_f32", "o2mi_radial_backward_workspace_bytes",
+                 "o2mi_radial_backward_f32"):
+        assert hasattr(lib, name)
+
+
+def test_radial_plan_create_validation():
+    import ctypes
+    from ictc_o2_hp import _native
+    try:
+        lib = _native.library()
+    except _native.NativeLibraryError:
+        pytest.skip("library not built")
+    handle = ctypes.c_void_p()
+    assert lib.o2mi_radial_plan_create(64, 4, 0, 4, 0, 64, ctypes.byref(handle)) == 0
+    assert lib.o2mi_radial_paths(handle) == 31
+    assert lib.o2mi_radial_plan_destroy(handle) == 0
+    assert lib.o2mi_radial_plan_create(24, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -2
+    assert lib.o2mi_radial_plan_create(64, 4, 0, 4, 0, 66, ctypes.byref(handle)) == -2
+    assert lib.o2mi_radial_plan_create(64, 4, 0, 4, 0, 128, ctypes.byref(handle)) == -2
+    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 0, 64, ctypes.byref(handle)) == -2
+    assert lib.o2mi_radial_plan_create(0, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -1
+    assert lib.o2mi_radial_plan_create(64, 4, 2, 4, 0, 64, ctypes.byref(handle)) == -1
+    assert lib.o2mi_radial_backward_workspace_bytes(None, 10, 31) == 0
