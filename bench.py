@@ -1,5 +1,10 @@
 """Benchmark of the headline hot path: TensorProduct fwd + full VJP on MI355X.
 
+``--workload radial`` and ``--workload uvu`` measure BASELINE.json configs[4]
+(RadialUvuTensorProduct chain) and configs[3] (UvuTensorProduct, at a row
+count that fits one GPU) with the same JSON fields; the default is the
+headline TensorProduct workload below.
+
 Workload (BASELINE.json metric): TensorProduct(C=128, m_max=6, parity="full"),
 N = 131072 rows, fp32, x, y ~ N(0, 1) and a materialised ones cotangent, all
 resident in HBM before timing.  One step = the compiled module's forward plus
@@ -44,6 +49,10 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="time budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu"))
+    p.add_argument("--edges", type=int, default=1048576, help="radial workload: edges")
+    p.add_argument("--uvu-rows", type=int, default=16384,
+                   help="uvu workload: rows (65536 needs 524 GB of per-row weights)")
     return p.parse_args()
 
 
@@ -85,12 +94,202 @@ def _traffic(path: Path, key: str):
         return None
 
 
+def _timed_steps(torch, step, steps, warmup):
+    """Warm up, then time `steps` steps with events on torch's current stream
+    (the stream every kernel of the step is launched on)."""
+    from ictc_o2_hp import _native
+    for _ in range(max(1, warmup)):
+        step()
+    torch.cuda.synchronize()
+    _native.kernel_timing_read_kinds()          # drop warm-up records
+    _native.kernel_timing(True)
+    start_evt = torch.cuda.Event(enable_timing=True)
+    stop_evt = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start_evt.record()
+    for _ in range(steps):
+        step()
+    stop_evt.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    _native.kernel_timing(False)
+    kinds = _native.kernel_timing_read_kinds()
+    return start_evt.elapsed_time(stop_evt) / steps, wall_ms / steps, kinds
+
+
+def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidden=64):
+    """gather x from nodes, Bessel(8) radial features with a cosine
+    cutoff -> MLP 8->64->64 (SiLU) -> fused final affine + V=1 uvu product."""
+    import math
+    from ictc_o2_hp import RadialUvuTensorProduct, UvuTensorProduct
+
+    tp = UvuTensorProduct(channels, 1, m_max, parity="canonical", shared_weights=False)
+    trunk = torch.nn.Sequential(torch.nn.Linear(8, hidden), torch.nn.SiLU(),
+                                torch.nn.Linear(hidden, hidden), torch.nn.SiLU())
+    radial_out = torch.nn.Linear(hidden, tp.weight_numel)
+
+    class Chain(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.trunk = trunk
+            self.radial = RadialUvuTensorProduct(tp, radial_out)
+
+        def forward(self, node_feats, src, basis, angular):
+            return self.radial(node_feats[src], angular, self.trunk(basis))
+
+    chain = Chain().to(device)
+    gen = torch.Generator(device=device).manual_seed(4242)
+    node_feats = torch.randn((nodes, tp.input1_dimension), device=device, generator=gen)
+    node_feats.requires_grad_()
+    src = torch.randint(0, nodes, (edges,), device=device, generator=gen)
+    r = 0.5 + 4.5 * torch.rand((edges, 1), device=device, generator=gen)
+    cutoff = 5.0
+    n = torch.arange(1, 9, device=device, dtype=torch.float32)
+    envelope = 0.5 * (torch.cos(math.pi * r / cutoff) + 1.0)
+    basis = math.sqrt(2.0 / cutoff) * torch.sin(n * math.pi * r / cutoff) / r * envelope
+    phi = 2.0 * math.pi * torch.rand((edges, 1), device=device, generator=gen)
+    parts = [torch.ones_like(phi)]
+    for m in range(1, m_max + 1):
+        parts += [torch.cos(m * phi), torch.sin(m * phi)]
+    angular = torch.cat(parts, dim=1).contiguous()
+    return chain, tp, node_feats, src, basis.contiguous(), angular
+
+
+def _radial_cpu_baseline(channels, m_max, hidden, budget_s):
+    """The radial oracle (numpy fp64 restatement of the reference algebra):
+    affine + uvu forward and its full VJP on 512-edge chunks."""
+    import numpy as np
+    from oracle import uvu_oracle as U
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    plan = U.UvuOraclePlan(channels, 1, m_max, parity="canonical")
+    rng = np.random.default_rng(0)
+    chunk = 512
+    x = rng.standard_normal((chunk, plan.width1))
+    y = rng.standard_normal((chunk, plan.width2))
+    h = rng.standard_normal((chunk, hidden))
+    a = rng.standard_normal((plan.weight_numel, hidden)) / 8.0
+    b = rng.standard_normal(plan.weight_numel)
+    g = rng.standard_normal((chunk, plan.width1))
+    edges, start = 0, time.perf_counter()
+    while True:
+        U.radial_forward(plan, x, y, h, a, b)
+        U.radial_backward(plan, x, y, h, a, b, g)
+        edges += chunk
+        elapsed = time.perf_counter() - start
+        if elapsed >= budget_s:
+            break
+    return {"value": edges / elapsed, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"{edges} edges in {chunk}-edge chunks, radial affine + uvu C{channels} "
+                      f"m{m_max} canonical forward and VJP (x, y, hidden, alpha, bias), "
+                      f"numpy fp64, {elapsed:.1f} s"}
+
+
+def radial_main(args):
+    import torch
+    from ictc_o2_hp import _native
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.set_float32_matmul_precision("highest")
+    device = torch.device("cuda:0")
+    _native.library()
+    torch.manual_seed(2024)
+    edges = args.edges
+    chain, tp, node_feats, src, basis, angular = _radial_chain(torch, device, edges)
+    run = chain if args.no_compile else torch.compile(chain, fullgraph=True, dynamic=False)
+    params = [node_feats] + list(chain.parameters())
+    cot = torch.ones((edges, tp.input1_dimension), device=device)
+
+    def step():
+        out = run(node_feats, src, basis, angular)
+        return torch.autograd.grad(out, params, cot)
+
+    ms_per_step, wall_ms, kinds = _timed_steps(torch, step, args.steps, args.warmup)
+    pw, hidden, width = tp.weight_numel, 64, tp.input1_dimension
+    gemm = 2.0 * edges * pw * hidden                      # one affine map over all edges
+    per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in kinds}
+    flops = {"radial_forward": gemm, "radial_backward": 2 * gemm, "radial_weight": gemm}
+    tflops = {k: flops[k] / (per[k] * 1e-3) / 1e12 for k in flops if per[k] > 0}
+    dominant = max(flops, key=lambda k: per[k])
+    peak = 157.3
+    record = {
+        "metric": "radial chain fwd + full VJP edges/s (configs[4]); matrix-core TFLOP/s",
+        "value": edges / (ms_per_step * 1e-3), "unit": "edges/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: random src/r/phi (seeded), random-init MLP 8->64->64 and final "
+                "affine, ones cotangent",
+        "config": {"workload": f"RadialUvuTensorProduct C64 m4 canonical E={edges} "
+                               "(gather from 65536 nodes, MLP 8->64->64 SiLU) fwd+full VJP",
+                   "edges": edges, "channels": 64, "m_max": 4, "hidden": hidden,
+                   "weights_per_edge": pw, "compiled": not args.no_compile},
+        "kernels_ms": per, "kernels_TFLOPs": tflops, "wall_ms_per_step": wall_ms,
+        "roofline": {"bound": "mfma", "kernel": dominant,
+                     "achieved": tflops.get(dominant), "peak": peak, "unit": "TFLOP/s",
+                     "frac": (tflops.get(dominant) or 0.0) / peak, "traffic": None},
+    }
+    del chain, node_feats, basis, angular, cot
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        record["cpu_baseline"] = _radial_cpu_baseline(64, 4, hidden, args.cpu_seconds)
+    print(json.dumps(record), flush=True)
+
+
+def uvu_main(args):
+    """configs[3] at a row count that fits one GPU: UvuTensorProduct C1=128,
+    C2=32, m4 full, per-row weights N(0, 1/sqrt(C2)), fwd + VJP with dw."""
+    import torch
+    from ictc_o2_hp import UvuTensorProduct, _native
+
+    device = torch.device("cuda:0")
+    _native.library()
+    n = args.uvu_rows
+    module = UvuTensorProduct(128, 32, 4, parity="full", shared_weights=False).to(device)
+    gen = torch.Generator(device=device).manual_seed(3131)
+    x = torch.randn((n, module.input1_dimension), device=device, generator=gen)
+    y = torch.randn((n, module.input2_dimension), device=device, generator=gen)
+    w = torch.randn((n, module.weight_numel), device=device, generator=gen) / (32 ** 0.5)
+    for t in (x, y, w):
+        t.requires_grad_()
+    cot = torch.ones_like(x)
+    run = module if args.no_compile else torch.compile(module, fullgraph=True, dynamic=False)
+
+    def step():
+        return torch.autograd.grad(run(x, y, w), (x, y, w), cot)
+
+    ms_per_step, wall_ms, _ = _timed_steps(torch, step, args.steps, args.warmup)
+    w1, w2, pw = module.input1_dimension, module.input2_dimension, module.weight_numel
+    # Algorithmic bytes: forward reads x, y, w, writes out; backward reads x, y,
+    # w, g and writes dx, dy, dw.
+    alg = 4.0 * n * (2 * w1 + w2 + pw + w1) + 4.0 * n * (3 * w1 + w2 + pw + w1 + w2 + pw)
+    achieved = alg / (ms_per_step * 1e-3) / 1e9
+    record = {
+        "metric": "uvu fwd + VJP rows/s (configs[3] shape, reduced N); step HBM GB/s",
+        "value": n / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: x, y ~ N(0,1), w ~ N(0, 1/sqrt(32)) per row (seeded), ones cotangent",
+        "config": {"workload": f"UvuTensorProduct C128 V32 m4 full N={n} per-row weights "
+                               "fwd+VJP (x, y, w)", "rows": n, "weights_per_row": pw},
+        "wall_ms_per_step": wall_ms,
+        "roofline": {"bound": "hbm", "kernel": "uvu step", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None},
+    }
+    print(json.dumps(record), flush=True)
+
+
 def main():
     args = _args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         raise SystemExit(2)
+    if args.workload == "radial":
+        return radial_main(args)
+    if args.workload == "uvu":
+        return uvu_main(args)
     import torch
     from ictc_o2_hp import TensorProduct, _native
 

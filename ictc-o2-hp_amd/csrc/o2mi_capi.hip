@@ -33,6 +33,43 @@ std::string& o2mi_error_slot() {
   return message;
 }
 
+// Optional kernel timing: while enabled, every timed call records a HIP event
+// pair around its main kernel on the call's stream.  Calls may come from any
+// thread (the autograd engine runs backward on its own).
+namespace {
+std::mutex g_timing_mu;
+bool g_timing = false;
+std::vector<O2miTimed> g_timed;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+bool o2mi_timing_begin(hipStream_t s, O2miTimed* launch, int kind) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  if (!g_timing) return false;
+  launch->kind = kind;
+  launch->start = take_event();
+  launch->stop = take_event();
+  if (!launch->start || !launch->stop) return false;
+  return hipEventRecord(launch->start, s) == hipSuccess;
+}
+
+void o2mi_timing_end(hipStream_t s, O2miTimed* launch) {
+  if (hipEventRecord(launch->stop, s) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timed.push_back(*launch);
+}
+
 namespace {
 
 int fail(int status, const std::string& message) {
@@ -183,47 +220,6 @@ hipError_t column_sum(const float* in, int64_t nrows, int64_t ncols, int64_t spl
   return hipGetLastError();
 }
 
-// Optional kernel timing: while enabled, every forward/backward call records
-// a HIP event pair around its main kernel on the call's stream.  Calls may
-// come from any thread (the autograd engine runs backward on its own).
-struct TimedLaunch {
-  int kind;  // 0 forward, 1 backward
-  hipEvent_t start, stop;
-};
-
-std::mutex g_timing_mu;
-bool g_timing = false;
-std::vector<TimedLaunch> g_timed;
-std::vector<hipEvent_t> g_event_pool;
-
-hipEvent_t take_event() {
-  if (!g_event_pool.empty()) {
-    hipEvent_t e = g_event_pool.back();
-    g_event_pool.pop_back();
-    return e;
-  }
-  hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
-  return e;
-}
-
-// Returns the start event to record (or nullptr when timing is off).
-bool timing_begin(hipStream_t s, TimedLaunch* launch, int kind) {
-  std::lock_guard<std::mutex> lock(g_timing_mu);
-  if (!g_timing) return false;
-  launch->kind = kind;
-  launch->start = take_event();
-  launch->stop = take_event();
-  if (!launch->start || !launch->stop) return false;
-  return hipEventRecord(launch->start, s) == hipSuccess;
-}
-
-void timing_end(hipStream_t s, TimedLaunch* launch) {
-  if (hipEventRecord(launch->stop, s) != hipSuccess) return;
-  std::lock_guard<std::mutex> lock(g_timing_mu);
-  g_timed.push_back(*launch);
-}
-
 }  // namespace
 
 extern "C" {
@@ -234,36 +230,47 @@ int o2mi_kernel_timing(int enable) {
   return O2MI_OK;
 }
 
-int o2mi_kernel_timing_read(double* forward_ms, int* forward_count, double* backward_ms,
-                            int* backward_count) {
-  std::vector<TimedLaunch> done;
+int o2mi_kernel_timing_read_kinds(double* ms, int* counts, int n_kinds) {
+  std::vector<O2miTimed> done;
   {
     std::lock_guard<std::mutex> lock(g_timing_mu);
     done.swap(g_timed);
   }
-  double totals[2] = {0.0, 0.0};
-  int counts[2] = {0, 0};
+  for (int k = 0; k < n_kinds; ++k) {
+    if (ms) ms[k] = 0.0;
+    if (counts) counts[k] = 0;
+  }
   int status = O2MI_OK;
-  for (const TimedLaunch& t : done) {
-    float ms = 0.f;
+  for (const O2miTimed& t : done) {
+    float elapsed = 0.f;
     if (hipEventSynchronize(t.stop) == hipSuccess &&
-        hipEventElapsedTime(&ms, t.start, t.stop) == hipSuccess) {
-      totals[t.kind] += ms;
-      counts[t.kind] += 1;
+        hipEventElapsedTime(&elapsed, t.start, t.stop) == hipSuccess) {
+      if (t.kind < n_kinds) {
+        if (ms) ms[t.kind] += elapsed;
+        if (counts) counts[t.kind] += 1;
+      }
     } else {
       status = fail(O2MI_ERR_HIP, "kernel timing: event query failed");
     }
   }
   {
     std::lock_guard<std::mutex> lock(g_timing_mu);
-    for (const TimedLaunch& t : done) {
+    for (const O2miTimed& t : done) {
       g_event_pool.push_back(t.start);
       g_event_pool.push_back(t.stop);
     }
   }
-  if (forward_ms) *forward_ms = totals[0];
+  return status;
+}
+
+int o2mi_kernel_timing_read(double* forward_ms, int* forward_count, double* backward_ms,
+                            int* backward_count) {
+  double ms[2];
+  int counts[2];
+  const int status = o2mi_kernel_timing_read_kinds(ms, counts, 2);
+  if (forward_ms) *forward_ms = ms[0];
   if (forward_count) *forward_count = counts[0];
-  if (backward_ms) *backward_ms = totals[1];
+  if (backward_ms) *backward_ms = ms[1];
   if (backward_count) *backward_count = counts[1];
   return status;
 }
@@ -367,10 +374,10 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
   const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
   int grid = 0;
   const o2mi::TPGeom g = geometry(plan, n_rows, target, o2mi::kForwardTile, &grid);
-  TimedLaunch timed;
-  const bool timing = timing_begin(s, &timed, 0);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_FORWARD);
   const hipError_t err = plan->set->forward(variant, x, y, w, out, g, grid, s);
-  if (timing) timing_end(s, &timed);
+  if (timing) o2mi_timing_end(s, &timed);
   if (err != hipSuccess) return fail_hip(err, "tp forward launch");
   return O2MI_OK;
 }
@@ -430,11 +437,11 @@ int o2mi_tp_backward_f32(const o2mi_tp_plan* plan, const float* x, const float* 
   if ((needed & 4) && (!workspace || workspace_bytes < shape.bytes))
     return fail(O2MI_ERR_WORKSPACE, "workspace smaller than o2mi_tp_backward_workspace_bytes");
   float* partial = static_cast<float*>(workspace);
-  TimedLaunch timed;
-  const bool timing = timing_begin(s, &timed, 1);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_BACKWARD);
   hipError_t err = plan->set->backward(variant, x, y, w, g, dx, dy, partial, shape.geom,
                                        shape.grid, needed, s);
-  if (timing) timing_end(s, &timed);
+  if (timing) o2mi_timing_end(s, &timed);
   if (err != hipSuccess) return fail_hip(err, "tp backward launch");
   if (needed & 4) {
     const int64_t pw = plan->weight_numel;

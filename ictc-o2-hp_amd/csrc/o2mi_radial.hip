@@ -155,7 +155,11 @@ int o2mi_radial_forward_f32(const o2mi_radial_plan* plan, const float* x, const 
   if (int st = check_inputs(x, y, hidden, alpha, bias, coefficients)) return st;
   if (!aligned16(out)) return fail(O2MI_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
   const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
-  const hipError_t err = plan->set->forward(a, out, static_cast<hipStream_t>(stream));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_FORWARD);
+  const hipError_t err = plan->set->forward(a, out, s);
+  if (timing) o2mi_timing_end(s, &timed);
   return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial forward launch");
 }
 
@@ -202,7 +206,10 @@ int o2mi_radial_backward_f32(const o2mi_radial_plan* plan, const float* x, const
     return fail(O2MI_ERR_INVALID_ARGUMENT, "galpha must be 16-byte aligned");
   const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
   if (needed & 7) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_BACKWARD);
     const hipError_t err = plan->set->backward(a, grad_output, gx, gy, ghidden, needed & 7, s);
+    if (timing) o2mi_timing_end(s, &timed);
     if (err != hipSuccess) return fail_hip(err, "radial backward launch");
   }
   if (needed & 24) {
@@ -215,7 +222,10 @@ int o2mi_radial_backward_f32(const o2mi_radial_plan* plan, const float* x, const
                   "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
     float* part_alpha = static_cast<float*>(workspace);
     float* part_bias = part_alpha + (int64_t)slices * rows * plan->H;
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_WEIGHT);
     hipError_t err = plan->set->weight(a, grad_output, per, slices, part_alpha, part_bias, s);
+    if (timing) o2mi_timing_end(s, &timed);
     if (err != hipSuccess) return fail_hip(err, "radial weight launch");
     if (needed & 8)
       hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows * plan->H)), dim3(256), 0, s,

@@ -91,6 +91,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_kernel_timing_read.restype = c_int
     lib.o2mi_kernel_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int),
                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int)]
+    lib.o2mi_kernel_timing_read_kinds.restype = c_int
+    lib.o2mi_kernel_timing_read_kinds.argtypes = [ctypes.POINTER(ctypes.c_double),
+                                                  ctypes.POINTER(c_int), c_int]
 
 
 def library() -> ctypes.CDLL:
@@ -198,3 +201,15 @@ def kernel_timing_read():
                                             ctypes.byref(b_ms), ctypes.byref(b_n)),
           "o2mi_kernel_timing_read")
     return f_ms.value, f_n.value, b_ms.value, b_n.value
+
+
+TIMED_KINDS = ("tp_forward", "tp_backward", "radial_forward", "radial_backward", "radial_weight")
+
+
+def kernel_timing_read_kinds() -> dict:
+    """{kind: (total_ms, count)} of the launches timed since the previous read."""
+    n = len(TIMED_KINDS)
+    ms = (ctypes.c_double * n)()
+    counts = (ctypes.c_int * n)()
+    check(library().o2mi_kernel_timing_read_kinds(ms, counts, n), "o2mi_kernel_timing_read_kinds")
+    return {kind: (ms[i], counts[i]) for i, kind in enumerate(TIMED_KINDS)}

@@ -184,6 +184,10 @@ int o2mi_radial_backward_f32(const o2mi_radial_plan *plan, const float *x, const
 int o2mi_kernel_timing(int enable);
 int o2mi_kernel_timing_read(double *forward_ms, int *forward_count, double *backward_ms,
                             int *backward_count);
+/* Same, per kind: 0 TP forward, 1 TP backward, 2 radial forward, 3 radial
+ * input adjoints (dx, dy, dhidden), 4 radial affine adjoints (dalpha, dbias).
+ * ms[k] and counts[k] for k < n_kinds. */
+int o2mi_kernel_timing_read_kinds(double *ms, int *counts, int n_kinds);
 
 #ifdef __cplusplus
 }
