@@ -234,6 +234,196 @@ __global__ __launch_bounds__(256) void uvu_weight_shared_kernel(
   partial[(int64_t)blockIdx.z * pr.wnum + r.wo + uv] = acc;
 }
 
+// ---- Per-row weights, V a multiple of 4 with V/4 dividing 64 ---------------
+// The weight stream ([N][P][C][V], 4 bytes per (row, path, u, v)) dominates:
+// one block per row reads that row's weights once, 16 bytes per lane per
+// load.  Within a path, lane q covers (u = q / G, v = 4 (q % G) .. +3) with
+// G = V / 4, so an aligned group of G lanes holds one u and the projection
+// sum_v w[u, v] y[v, :] finishes with log2(G) xor shuffles.  Thread t
+// handles q = t + 256 i for every path, so it always owns the same u values:
+// the row's output (forward) and dx (backward) accumulators live in LDS with
+// a single writer per element and need no atomics.  x, y and g of the row are
+// staged in LDS.  Coupling slot order is [out c][in1 a][in2 b].
+constexpr int kRowThreads = 256;
+using f4v = float __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float group_sum(float v, int group) {
+  for (int o = 1; o < group; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+struct RowPath {
+  PathRec r;
+  float c[8];
+};
+
+__device__ __forceinline__ RowPath row_path(const Problem& pr, int p) {
+  RowPath rp;
+  rp.r = path_rec(pr, p);
+  for (int k = 0; k < 8; ++k) rp.c[k] = pr.coef[8 * p + k];
+  return rp;
+}
+
+// sum_v w[v] y[v, b] over this lane's 4 values of v.
+__device__ __forceinline__ void lane_project(const f4v wv, const float* sy, int yo, int yd,
+                                             int v0, float& p0, float& p1) {
+  if (yd == 2) {
+    const float* yv = sy + yo + 2 * v0;
+    p0 = wv.x * yv[0] + wv.y * yv[2] + wv.z * yv[4] + wv.w * yv[6];
+    p1 = wv.x * yv[1] + wv.y * yv[3] + wv.z * yv[5] + wv.w * yv[7];
+  } else {
+    const float* yv = sy + yo + v0;
+    p0 = wv.x * yv[0] + wv.y * yv[1] + wv.z * yv[2] + wv.w * yv[3];
+    p1 = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void uvu_row_forward_kernel(
+    Problem pr, const float* __restrict__ x, const float* __restrict__ y,
+    const float* __restrict__ w, float* __restrict__ out) {
+  extern __shared__ float s_row[];
+  float* sx = s_row;
+  float* sy = sx + pr.W1;
+  float* so = sy + pr.W2;
+  const int64_t n = blockIdx.x;
+  for (int i = threadIdx.x; i < pr.W1; i += kRowThreads) {
+    sx[i] = x[n * pr.W1 + i];
+    so[i] = 0.f;
+  }
+  for (int i = threadIdx.x; i < pr.W2; i += kRowThreads) sy[i] = y[n * pr.W2 + i];
+  __syncthreads();
+  const int G = pr.V / 4;
+  const int per_path = pr.C * G;
+  const f4v* wrow = reinterpret_cast<const f4v*>(w + n * pr.wnum);
+  for (int p = 0; p < pr.P; ++p) {
+    const RowPath rp = row_path(pr, p);
+    const f4v* wp = wrow + rp.r.wo / 4;
+    for (int q = threadIdx.x; q < per_path; q += kRowThreads) {
+      const f4v wv = __builtin_nontemporal_load(wp + q);
+      const int u = q / G, v0 = 4 * (q - u * G);
+      float p0, p1;
+      lane_project(wv, sy, rp.r.yo, rp.r.yd, v0, p0, p1);
+      p0 = group_sum(p0, G);
+      p1 = group_sum(p1, G);
+      if (v0 == 0) {
+        const float a0 = sx[rp.r.xo + u * rp.r.xd];
+        const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
+        float* o = so + rp.r.oo + u * rp.r.od;
+        const float* c = rp.c;
+        o[0] += a0 * (c[0] * p0 + c[1] * p1) + a1 * (c[2] * p0 + c[3] * p1);
+        if (rp.r.od == 2) o[1] += a0 * (c[4] * p0 + c[5] * p1) + a1 * (c[6] * p0 + c[7] * p1);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < pr.W1; i += kRowThreads) out[n * pr.W1 + i] = so[i];
+}
+
+// dx (bit 1), dy (bit 2) and per-row dw (bit 4) in one pass over the row's
+// weights.  Paths are visited grouped by second-input entry (second_order),
+// so each lane keeps its dy partials for its 4 values of v in registers for
+// one entry at a time; they are summed over u by shuffles (lanes with equal
+// q % G) and over the 4 waves in LDS, in a fixed order.
+__global__ __launch_bounds__(kRowThreads) void uvu_row_backward_kernel(
+    Problem pr, const float* __restrict__ x, const float* __restrict__ y,
+    const float* __restrict__ w, const float* __restrict__ g, float* __restrict__ gx,
+    float* __restrict__ gy, float* __restrict__ gw, int needed) {
+  extern __shared__ float s_row[];
+  float* sx = s_row;
+  float* sg = sx + pr.W1;
+  float* sdx = sg + pr.W1;
+  float* sy = sdx + pr.W1;
+  float* sdy = sy + pr.W2;  // [4 waves][W2]
+  const int64_t n = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < pr.W1; i += kRowThreads) {
+    sx[i] = x[n * pr.W1 + i];
+    sg[i] = g[n * pr.W1 + i];
+    sdx[i] = 0.f;
+  }
+  for (int i = threadIdx.x; i < pr.W2; i += kRowThreads) sy[i] = y[n * pr.W2 + i];
+  __syncthreads();
+  const bool want_x = needed & 1, want_y = (needed & 2) != 0, want_w = (needed & 4) != 0;
+  const bool read_w = want_x || want_y;
+  const int G = pr.V / 4;
+  const int per_path = pr.C * G;
+  const f4v* wrow = reinterpret_cast<const f4v*>(w + n * pr.wnum);
+  f4v* dwrow = reinterpret_cast<f4v*>(gw + n * pr.wnum);
+  for (int j = 0; j < pr.NY; ++j) {
+    int yo, yd, begin, end;
+    entry_rec(pr, 2, j, yo, yd, begin, end);
+    float dy[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+    for (int k = begin; k < end; ++k) {
+      const RowPath rp = row_path(pr, pr.order2[k]);
+      const float* c = rp.c;
+      for (int q = threadIdx.x; q < per_path; q += kRowThreads) {
+        const int u = q / G, v0 = 4 * (q - u * G);
+        const float a0 = sx[rp.r.xo + u * rp.r.xd];
+        const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
+        const float g0 = sg[rp.r.oo + u * rp.r.od];
+        const float g1 = rp.r.od == 2 ? sg[rp.r.oo + u * rp.r.od + 1] : 0.f;
+        // r_b = d out / d proj_b for this (row, path, u).
+        const float r0 = a0 * (c[0] * g0 + c[4] * g1) + a1 * (c[2] * g0 + c[6] * g1);
+        const float r1 = a0 * (c[1] * g0 + c[5] * g1) + a1 * (c[3] * g0 + c[7] * g1);
+        const float* yv = sy + yo + yd * v0;
+        if (want_w) {
+          f4v d;
+          if (yd == 2) {
+            d.x = r0 * yv[0] + r1 * yv[1];
+            d.y = r0 * yv[2] + r1 * yv[3];
+            d.z = r0 * yv[4] + r1 * yv[5];
+            d.w = r0 * yv[6] + r1 * yv[7];
+          } else {
+            d.x = r0 * yv[0];
+            d.y = r0 * yv[1];
+            d.z = r0 * yv[2];
+            d.w = r0 * yv[3];
+          }
+          __builtin_nontemporal_store(d, dwrow + rp.r.wo / 4 + q);
+        }
+        if (read_w) {
+          const f4v wv = __builtin_nontemporal_load(wrow + rp.r.wo / 4 + q);
+          dy[0][0] += wv.x * r0; dy[0][1] += wv.x * r1;
+          dy[1][0] += wv.y * r0; dy[1][1] += wv.y * r1;
+          dy[2][0] += wv.z * r0; dy[2][1] += wv.z * r1;
+          dy[3][0] += wv.w * r0; dy[3][1] += wv.w * r1;
+          if (want_x) {
+            float p0, p1;
+            lane_project(wv, sy, yo, yd, v0, p0, p1);
+            p0 = group_sum(p0, G);
+            p1 = group_sum(p1, G);
+            if (v0 == 0) {
+              float* d = sdx + rp.r.xo + u * rp.r.xd;
+              d[0] += g0 * (c[0] * p0 + c[1] * p1) + g1 * (c[4] * p0 + c[5] * p1);
+              if (rp.r.xd == 2) d[1] += g0 * (c[2] * p0 + c[3] * p1) + g1 * (c[6] * p0 + c[7] * p1);
+            }
+          }
+        }
+      }
+    }
+    if (want_y) {
+      // Sum over the lanes of this wave that share v0 (equal lane % G).
+      for (int o = G; o < 64; o <<= 1)
+        for (int v = 0; v < 4; ++v) {
+          dy[v][0] += __shfl_xor(dy[v][0], o, 64);
+          dy[v][1] += __shfl_xor(dy[v][1], o, 64);
+        }
+      if (lane < G) {
+        for (int v = 0; v < 4; ++v) {
+          sdy[wave * pr.W2 + yo + yd * (4 * lane + v)] = dy[v][0];
+          if (yd == 2) sdy[wave * pr.W2 + yo + yd * (4 * lane + v) + 1] = dy[v][1];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (want_x)
+    for (int i = threadIdx.x; i < pr.W1; i += kRowThreads) gx[n * pr.W1 + i] = sdx[i];
+  if (want_y)
+    for (int i = threadIdx.x; i < pr.W2; i += kRowThreads)
+      gy[n * pr.W2 + i] = (sdy[i] + sdy[pr.W2 + i]) + (sdy[2 * pr.W2 + i] + sdy[3 * pr.W2 + i]);
+}
+
 __global__ __launch_bounds__(256) void uvu_column_sum_kernel(const float* __restrict__ in,
                                                              int64_t rows, int64_t cols,
                                                              float* __restrict__ out) {
@@ -288,6 +478,20 @@ int64_t shared_splits(const Problem& pr) {
 
 unsigned blocks_for(int64_t items) { return (unsigned)((items + 255) / 256); }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// LDS bytes of the per-row kernels, or 0 when they do not apply: per-row
+// weights, V = 4 G with G dividing 64, 16-byte aligned weight rows and row
+// state within the default 64 KB of dynamic LDS.
+size_t row_kernel_lds(const Problem& pr, bool backward, const void* w, const void* gw) {
+  if (pr.shared || pr.V % 4 != 0 || 64 % (pr.V / 4) != 0 || pr.n > 0x7fffffff) return 0;
+  if ((w && !aligned16(w)) || (gw && !aligned16(gw))) return 0;
+  const size_t floats = backward ? (size_t)3 * pr.W1 + (size_t)5 * pr.W2
+                                 : (size_t)2 * pr.W1 + (size_t)pr.W2;
+  const size_t bytes = floats * sizeof(float);
+  return bytes <= 65536 ? bytes : 0;
+}
+
 }  // namespace uvu
 }  // namespace o2mi
 
@@ -302,6 +506,12 @@ int o2mi_uvu_forward_f32(const o2mi_uvu_problem* problem, const float* x, const 
   if (pr.n == 0) return O2MI_OK;
   if (!x || !y || !w || !out) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (const size_t lds = row_kernel_lds(pr, false, w, nullptr)) {
+    hipLaunchKernelGGL(uvu_row_forward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
+                       pr, x, y, w, out);
+    return hipGetLastError() == hipSuccess ? O2MI_OK
+                                           : fail(O2MI_ERR_HIP, "uvu forward launch failed");
+  }
   hipLaunchKernelGGL(uvu_forward_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr, x,
                      y, w, out);
   return hipGetLastError() == hipSuccess ? O2MI_OK
@@ -333,6 +543,12 @@ int o2mi_uvu_backward_f32(const o2mi_uvu_problem* problem, const float* x, const
   if (!x || !y || !w || !g) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
   if (((needed & 1) && !gx) || ((needed & 2) && !gy) || ((needed & 4) && !gw))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
+  if (const size_t lds = row_kernel_lds(pr, true, w, (needed & 4) ? gw : nullptr)) {
+    hipLaunchKernelGGL(uvu_row_backward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
+                       pr, x, y, w, g, gx, gy, gw, needed);
+    return hipGetLastError() == hipSuccess ? O2MI_OK
+                                           : fail(O2MI_ERR_HIP, "uvu backward launch failed");
+  }
   if ((needed & 1) || ((needed & 4) && !pr.shared)) {
     hipLaunchKernelGGL(uvu_backward_x_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr,
                        x, y, w, g, gx, gw, needed);

@@ -52,6 +52,12 @@ CASES = [
     (5, 2, 3, {"parity": "canonical", "m_max_in2": 1, "path_normalization": "path"}, False, 33),
     (7, 3, 1, {"parity": "full", "normalization": "norm", "path_normalization": "element"},
      True, 1),
+    # Per-row weights with V = 4 G, G | 64: the row-streaming kernels.
+    (7, 4, 4, {"parity": "full", "m_max_in2": 2}, False, 17),                  # G = 1
+    (5, 8, 3, {"parity": "full"}, False, 30),                                  # G = 2
+    (12, 16, 2, {"parity": "canonical", "parity_in2": "full"}, False, 20),     # G = 4
+    (3, 64, 2, {"parity": "full", "path_normalization": "path"}, False, 10),   # G = 16
+    (2, 256, 1, {"parity": "canonical"}, False, 5),                            # G = 64
 ]
 
 
@@ -65,6 +71,7 @@ def test_uvu_parity(c, v, m, kw, shared, n):
 def test_uvu_gradient_roles(wrt):
     _case(12, 2, 3, {"parity": "full"}, False, 40, seed=5, wrt=wrt)
     _case(12, 2, 3, {"parity": "full"}, True, 40, seed=6, wrt=wrt)
+    _case(16, 8, 2, {"parity": "full"}, False, 33, seed=7, wrt=wrt)     # row kernels
 
 
 def test_uvu_golden_vectors(golden_uvu):
