@@ -50,6 +50,9 @@ def _args():
                    help="time budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu"))
+    p.add_argument("--copy-probe", action="store_true",
+                   help="after the run, copy 512 MiB 3 times with an elementwise kernel "
+                        "(reference traffic for HBM counter calibration)")
     p.add_argument("--edges", type=int, default=1048576, help="radial workload: edges")
     p.add_argument("--uvu-rows", type=int, default=16384,
                    help="uvu workload: rows (65536 needs 524 GB of per-row weights)")
@@ -286,10 +289,26 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         raise SystemExit(2)
-    if args.workload == "radial":
-        return radial_main(args)
-    if args.workload == "uvu":
-        return uvu_main(args)
+    if args.workload != "tp":
+        (radial_main if args.workload == "radial" else uvu_main)(args)
+        return _copy_probe(args)
+    tp_main(args)
+    _copy_probe(args)
+
+
+def _copy_probe(args):
+    """out = src * 1 over 2^27 floats: 512 MiB read + 512 MiB written per launch."""
+    if not args.copy_probe:
+        return
+    import torch
+    src = torch.ones(1 << 27, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+
+
+def tp_main(args):
     import torch
     from ictc_o2_hp import TensorProduct, _native
 
