@@ -12,10 +12,16 @@ from conftest import GOLDEN
 
 def test_public_names():
     import ictc_o2_hp
-    for name in ("TensorProduct", "TupleTensorProduct", "ComponentMajorTensorProduct",
-                 "ReferenceTensorProduct"):
+    # The reference's public names (__init__.py:4-25).
+    names = ("TensorProduct", "TupleTensorProduct", "ComponentMajorTensorProduct",
+             "ReferenceTensorProduct", "UvuTensorProduct", "ReferenceUvuTensorProduct",
+             "RadialUvuTensorProduct")
+    for name in names:
         assert getattr(ictc_o2_hp, name) is not None
+    assert set(names) <= set(ictc_o2_hp.__all__)
     assert ictc_o2_hp.__version__ == "0.1.6.dev0"
+    with pytest.raises(AttributeError):
+        ictc_o2_hp.NotAnOperator
 
 
 @pytest.mark.parametrize("args", [(0, 2), (1.5, 2), (4, -1), (4, 1.5)])
