@@ -193,7 +193,8 @@ struct BackwardShape {
 BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant) {
   BackwardShape s{};
   s.variant = variant;
-  const int64_t target = (int64_t)p->set->blocks_per_cu(variant, true) * device_cus();
+  const int64_t target =
+      (int64_t)p->set->blocks_per_cu(variant, true) * device_cus() * O2MI_BWD_BLOCKS_MULT;
   s.geom = geometry(p, n_rows, target, o2mi::kBackwardTile, &s.grid);
   s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
   s.splits = s.partial_rows <= kReduceSplitRows
@@ -371,7 +372,8 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
     return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int variant = pick_variant(plan, {x, y, out});
-  const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
+  const int64_t target =
+      (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus() * O2MI_FWD_BLOCKS_MULT;
   int grid = 0;
   const o2mi::TPGeom g = geometry(plan, n_rows, target, o2mi::kForwardTile, &grid);
   O2miTimed timed;

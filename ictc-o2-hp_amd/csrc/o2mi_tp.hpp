@@ -80,6 +80,18 @@ struct TermSpec {
 #ifndef O2MI_BWD_TILE
 #define O2MI_BWD_TILE 256  // lanes of one row handled by a backward block
 #endif
+// Blocks launched per resident block slot (1: persistent kernels).
+// 1: the forward keeps each lane's path weights in registers for the whole
+// (persistent) kernel instead of re-reading them from LDS every row.
+#ifndef O2MI_FWD_WREG
+#define O2MI_FWD_WREG 1
+#endif
+#ifndef O2MI_FWD_BLOCKS_MULT
+#define O2MI_FWD_BLOCKS_MULT 1
+#endif
+#ifndef O2MI_BWD_BLOCKS_MULT
+#define O2MI_BWD_BLOCKS_MULT 1
+#endif
 #ifndef O2MI_ROW_ORDER
 #define O2MI_ROW_ORDER 1  // 1: block b takes iterations b, b+G, ...; 0: one contiguous range
 #endif
@@ -412,9 +424,20 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
   const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
+#if O2MI_FWD_WREG
+  // This lane's weight of every path (times the coupling magnitude).
+  float wreg[P::kPaths];
+  static_for<P::kPaths>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr PathSpec ps = P::paths[p];
+    const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
+    wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
+  });
+#else
   stage_weights<P, kTile>(lds_w, w, C, tile);
   __syncthreads();
   WeightColumns<P> col = weight_columns<P>(l);
+#endif
 
   const RowSchedule sched = row_schedule(g, group);
   float X[P::kKeys][2], Y[P::kKeys][2];
@@ -437,9 +460,11 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
       load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
       load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
     }
+#if !O2MI_FWD_WREG
     // Re-read the weights every iteration: keeping all of them in registers
     // would cost occupancy.
     asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
+#endif
     float A[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       A[decltype(kc)::value][0] = 0.f;
@@ -448,7 +473,11 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
+#if O2MI_FWD_WREG
+      const float wv = wreg[p];
+#else
       const float wv = staged_weight<P, kTile, p>(lds_w, col);
+#endif
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       A[ps.k3][0] = fmaf(wv, f0, A[ps.k3][0]);

@@ -58,7 +58,7 @@ hipError_t launch_forward(const float* x, const float* y, const float* w, float*
                           const TPGeom& g, int grid, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
-  const size_t lds = lds_bytes<P, kForwardTile>();
+  const size_t lds = O2MI_FWD_WREG ? 0 : lds_bytes<P, kForwardTile>();
   hipError_t err = allow_lds(kernel, lds, done);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
@@ -120,7 +120,7 @@ int occupancy_of(bool backward) {
       return 1;
   } else {
     const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
-    const size_t lds = lds_bytes<P, kForwardTile>();
+    const size_t lds = O2MI_FWD_WREG ? 0 : lds_bytes<P, kForwardTile>();
     if (allow_lds(kernel, lds, done_f) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
