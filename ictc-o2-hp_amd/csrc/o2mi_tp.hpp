@@ -86,6 +86,22 @@ struct TermSpec {
 #ifndef O2MI_FWD_WREG
 #define O2MI_FWD_WREG 1
 #endif
+// Start delay, in units of s_sleep(127) (~8k cycles), of the blocks in the
+// second half of the grid (the second resident block of each CU), so that the
+// two blocks sharing a CU alternate between memory and compute phases.
+#ifndef O2MI_FWD_STAGGER
+#define O2MI_FWD_STAGGER 0
+#endif
+#ifndef O2MI_BWD_STAGGER
+#define O2MI_BWD_STAGGER 0
+#endif
+// Backward variants: weights in registers (no LDS) and/or no next-row prefetch.
+#ifndef O2MI_BWD_WREG
+#define O2MI_BWD_WREG 0
+#endif
+#ifndef O2MI_BWD_PREFETCH
+#define O2MI_BWD_PREFETCH 0
+#endif
 #ifndef O2MI_FWD_BLOCKS_MULT
 #define O2MI_FWD_BLOCKS_MULT 1
 #endif
@@ -394,6 +410,14 @@ struct RowSchedule {
   }
 };
 
+template <int kSleeps>
+__device__ __forceinline__ void stagger_start() {
+  if constexpr (kSleeps > 0) {
+    if (blockIdx.x >= gridDim.x / 2)
+      for (int i = 0; i < kSleeps; ++i) __builtin_amdgcn_s_sleep(127);
+  }
+}
+
 __device__ __forceinline__ RowSchedule row_schedule(const TPGeom& g, int64_t group) {
   RowSchedule s;
   s.rows_per_iter = g.rows_per_iter;
@@ -440,6 +464,7 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
 #endif
 
   const RowSchedule sched = row_schedule(g, group);
+  stagger_start<O2MI_FWD_STAGGER>();
   float X[P::kKeys][2], Y[P::kKeys][2];
   if constexpr (O2MI_FWD_PREFETCH) {
     load_row<P, kLayout, kVec2>(rows_rsrc(x, sched.row0(0), g.width, sched.rows(0)), C, l, o,
@@ -514,9 +539,19 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
   const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
+#if O2MI_BWD_WREG
+  float wreg[P::kPaths];
+  static_for<P::kPaths>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr PathSpec ps = P::paths[p];
+    const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
+    wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
+  });
+#else
   stage_weights<P, kTile>(lds_w, w, C, tile);
   __syncthreads();
   WeightColumns<P> col = weight_columns<P>(l);
+#endif
 
   float dwacc[P::kPaths];
   static_for<P::kPaths>([&](auto pc) { dwacc[decltype(pc)::value] = 0.f; });
@@ -527,6 +562,7 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
   if (!(needed & 1)) ox.scalar_own = ox.freq = kIdle;
   if (!(needed & 2)) oy.scalar_own = oy.freq = kIdle;
 
+  stagger_start<O2MI_BWD_STAGGER>();
   float X[P::kKeys][2], Y[P::kKeys][2], G[P::kKeys][2];
   {
     const int64_t row0 = sched.row0(0);
@@ -540,26 +576,40 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
   for (int it = 0; it < sched.iters; ++it) {
     const int64_t row0 = sched.row0(it);
     const int rows = sched.rows(it);
+#if O2MI_BWD_PREFETCH
     const int64_t row_next = sched.row0(it + 1);
     const int rows_next = sched.rows(it + 1);
     float Xn[P::kKeys][2], Yn[P::kKeys][2], Gn[P::kKeys][2];
     load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
     load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
     load_row<P, kLayout, kVec2>(rows_rsrc(gout, row_next, g.width, rows_next), C, l, o, true, Gn);
+#else
+    if (it > 0) {
+      load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
+      load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
+      load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
+    }
+#endif
 
     float DX[P::kKeys][2], DY[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       DX[k][0] = DX[k][1] = DY[k][0] = DY[k][1] = 0.f;
     });
+#if !O2MI_BWD_WREG
     // Re-read the weights from LDS every iteration: hoisting the loop-invariant
     // reads out of the loop would cost as many registers.
     asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
+#endif
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
       constexpr bool freq3 = out_is_freq<P>(p);
+#if O2MI_BWD_WREG
+      const float wv = wreg[p];
+#else
       const float wv = staged_weight<P, kTile, p>(lds_w, col);
+#endif
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       dwacc[p] = fmaf(G[ps.k3][0], f0, dwacc[p]);
@@ -584,6 +634,7 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
     store_row<P, kLayout, kVec2>(rows_rsrc(dx, row0, g.width, rows), C, l, ox, DX);
     store_row<P, kLayout, kVec2>(rows_rsrc(dy, row0, g.width, rows), C, l, oy, DY);
 
+#if O2MI_BWD_PREFETCH
     static_for<P::kKeys>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       X[k][0] = Xn[k][0];
@@ -593,6 +644,7 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
       G[k][0] = Gn[k][0];
       G[k][1] = Gn[k][1];
     });
+#endif
   }
 
   if ((needed & 4) && l.active) {

@@ -72,7 +72,7 @@ hipError_t launch_backward(const float* x, const float* y, const float* w, const
                            int needed, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-  const size_t lds = lds_bytes<P, kBackwardTile>();
+  const size_t lds = O2MI_BWD_WREG ? 0 : lds_bytes<P, kBackwardTile>();
   hipError_t err = allow_lds(kernel, lds, done);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((tp_backward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
@@ -113,7 +113,7 @@ int occupancy_of(bool backward) {
   static std::atomic<uint64_t> done_f{0}, done_b{0};
   if (backward) {
     const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-    const size_t lds = lds_bytes<P, kBackwardTile>();
+    const size_t lds = O2MI_BWD_WREG ? 0 : lds_bytes<P, kBackwardTile>();
     if (allow_lds(kernel, lds, done_b) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
