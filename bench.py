@@ -80,11 +80,31 @@ def _cpu_baseline(channels, m_max, parity, width, budget_s):
         port.forward_vjp(x, y, w, g)
         rows += chunk
         elapsed = time.perf_counter() - start
-        if elapsed >= budget_s or rows >= 16 * chunk:
+        if elapsed >= budget_s:
             break
     return {"value": rows / elapsed, "unit": "rows/s", "cores": cores, "kind": "port",
+            "cpu": _cpu_model(),
             "sample": f"{rows} rows in {chunk}-row chunks of C{channels} m{m_max} {parity}, "
                       f"fp32 forward + autograd dx/dy/dw, {elapsed:.1f} s"}
+
+
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _sample_stats(samples):
+    """Median and inter-quartile range of per-step times (ms)."""
+    import statistics
+    if not samples:
+        return None, None
+    q = statistics.quantiles(samples, n=4) if len(samples) >= 2 else [samples[0]] * 3
+    return statistics.median(samples), q[2] - q[0]
 
 
 def _traffic(path: Path, key: str):
@@ -106,19 +126,19 @@ def _timed_steps(torch, step, steps, warmup):
     torch.cuda.synchronize()
     _native.kernel_timing_read_kinds()          # drop warm-up records
     _native.kernel_timing(True)
-    start_evt = torch.cuda.Event(enable_timing=True)
-    stop_evt = torch.cuda.Event(enable_timing=True)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    start_evt.record()
-    for _ in range(steps):
+    events[0].record()
+    for i in range(steps):
         step()
-    stop_evt.record()
+        events[i + 1].record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     _native.kernel_timing(False)
     kinds = _native.kernel_timing_read_kinds()
-    return start_evt.elapsed_time(stop_evt) / steps, wall_ms / steps, kinds
+    samples = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return events[0].elapsed_time(events[-1]) / steps, wall_ms / steps, kinds, samples
 
 
 def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidden=64):
@@ -208,7 +228,8 @@ def radial_main(args):
         out = run(node_feats, src, basis, angular)
         return torch.autograd.grad(out, params, cot)
 
-    ms_per_step, wall_ms, kinds = _timed_steps(torch, step, args.steps, args.warmup)
+    ms_per_step, wall_ms, kinds, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    median, iqr = _sample_stats(samples)
     pw, hidden, width = tp.weight_numel, 64, tp.input1_dimension
     gemm = 2.0 * edges * pw * hidden                      # one affine map over all edges
     per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in kinds}
@@ -227,6 +248,7 @@ def radial_main(args):
                                "(gather from 65536 nodes, MLP 8->64->64 SiLU) fwd+full VJP",
                    "edges": edges, "channels": 64, "m_max": 4, "hidden": hidden,
                    "weights_per_edge": pw, "compiled": not args.no_compile},
+        "ms_per_step_median": median, "ms_per_step_iqr": iqr,
         "kernels_ms": per, "kernels_TFLOPs": tflops, "wall_ms_per_step": wall_ms,
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": tflops.get(dominant), "peak": peak, "unit": "TFLOP/s",
@@ -261,7 +283,8 @@ def uvu_main(args):
     def step():
         return torch.autograd.grad(run(x, y, w), (x, y, w), cot)
 
-    ms_per_step, wall_ms, _ = _timed_steps(torch, step, args.steps, args.warmup)
+    ms_per_step, wall_ms, _, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    median, iqr = _sample_stats(samples)
     w1, w2, pw = module.input1_dimension, module.input2_dimension, module.weight_numel
     # Algorithmic bytes: forward reads x, y, w, writes out; backward reads x, y,
     # w, g and writes dx, dy, dw.
@@ -275,6 +298,7 @@ def uvu_main(args):
         "data": "synthetic: x, y ~ N(0,1), w ~ N(0, 1/sqrt(32)) per row (seeded), ones cotangent",
         "config": {"workload": f"UvuTensorProduct C128 V32 m4 full N={n} per-row weights "
                                "fwd+VJP (x, y, w)", "rows": n, "weights_per_row": pw},
+        "ms_per_step_median": median, "ms_per_step_iqr": iqr,
         "wall_ms_per_step": wall_ms,
         "roofline": {"bound": "hbm", "kernel": "uvu step", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
@@ -331,24 +355,10 @@ def tp_main(args):
         out = run(x, y)
         return torch.autograd.grad(out, (x, y, module.weight), cot)
 
-    for _ in range(max(1, args.warmup)):
-        step()
-    torch.cuda.synchronize()
-    _native.kernel_timing_read()              # drop warm-up records
-    _native.kernel_timing(True)
-    start_evt = torch.cuda.Event(enable_timing=True)
-    stop_evt = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start_evt.record()
-    for _ in range(args.steps):
-        step()
-    stop_evt.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    _native.kernel_timing(False)
-    fwd_ms, fwd_n, bwd_ms, bwd_n = _native.kernel_timing_read()
-    ms_per_step = start_evt.elapsed_time(stop_evt) / args.steps
+    ms_per_step, wall_ms, kinds, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    wall_ms *= args.steps
+    median, iqr = _sample_stats(samples)
+    (fwd_ms, fwd_n), (bwd_ms, bwd_n) = kinds["tp_forward"], kinds["tp_backward"]
 
     alg_step = 4.0 * (8.0 * n * width + 3.0 * pw)
     alg_bwd = 4.0 * (5.0 * n * width + 2.0 * pw)
@@ -365,6 +375,8 @@ def tp_main(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_per_step,
+        "ms_per_step_median": median,
+        "ms_per_step_iqr": iqr,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": (n / (ms_per_step * 1e-3)) / A100_PUBLISHED_ROWS_S

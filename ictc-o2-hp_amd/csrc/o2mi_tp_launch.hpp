@@ -126,6 +126,8 @@ int occupancy_of(bool backward) {
             &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
       return 1;
   }
+  const int cap = backward ? O2MI_BWD_MAX_BLOCKS_PER_CU : O2MI_FWD_MAX_BLOCKS_PER_CU;
+  if (cap > 0 && blocks > cap) blocks = cap;
   return blocks > 0 ? blocks : 1;
 }
 
