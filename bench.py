@@ -49,7 +49,9 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="time budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu"))
+    p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu", "grid"),
+                   help="grid: every configs[2] point (and configs[1]) as HIP-graph replays")
+    p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
     p.add_argument("--copy-probe", action="store_true",
                    help="after the run, copy 512 MiB 3 times with an elementwise kernel "
                         "(reference traffic for HBM counter calibration)")
@@ -307,12 +309,155 @@ def uvu_main(args):
     print(json.dumps(record), flush=True)
 
 
+# Published A100 times (ms) of the reference's TensorProduct, forward and
+# forward + full VJP, for every configs[2] point
+# (benchmarks/eqx/results/complete_matrix.csv): "N C m_max parity fwd fwd+VJP".
+A100_GRID = (
+    "16384 32 1 c 0.0584 0.302; 16384 32 1 f 0.0809 0.442; 16384 32 4 c 0.2002 0.903;"
+    "16384 32 4 f 0.2074 1.376; 16384 32 6 c 0.3594 1.688; 16384 32 6 f 0.2816 2.399;"
+    "16384 64 1 c 0.0742 0.349; 16384 64 1 f 0.1188 0.636; 16384 64 4 c 0.1889 1.378;"
+    "16384 64 4 f 0.3471 2.500; 16384 64 6 c 0.2586 2.533; 16384 64 6 f 0.4864 4.596;"
+    "16384 128 1 c 0.0998 0.465; 16384 128 1 f 0.1966 1.030; 16384 128 4 c 0.3267 2.537;"
+    "16384 128 4 f 0.6528 4.884; 16384 128 6 c 0.4552 4.674; 16384 128 6 f 0.9083 7.824;"
+    "16384 256 1 c 0.1587 0.689; 16384 256 1 f 0.3564 1.977; 16384 256 4 c 0.6001 4.964;"
+    "16384 256 4 f 1.2252 9.202; 16384 256 6 c 0.8663 9.286; 16384 256 6 f 1.7613 15.263;"
+    "32768 32 1 c 0.0753 0.378; 32768 32 1 f 0.1188 0.647; 32768 32 4 c 0.3569 1.670;"
+    "32768 32 4 f 0.3523 2.500; 32768 32 6 c 0.6666 3.237; 32768 32 6 f 0.4931 4.575;"
+    "32768 64 1 c 0.1004 0.468; 32768 64 1 f 0.1961 1.029; 32768 64 4 c 0.3256 2.549;"
+    "32768 64 4 f 0.6385 4.836; 32768 64 6 c 0.4552 4.909; 32768 64 6 f 0.8980 8.370;"
+    "32768 128 1 c 0.1541 0.683; 32768 128 1 f 0.3512 1.973; 32768 128 4 c 0.5980 4.947;"
+    "32768 128 4 f 1.2518 9.512; 32768 128 6 c 0.8530 8.595; 32768 128 6 f 1.7444 15.108;"
+    "32768 256 1 c 0.2668 1.231; 32768 256 1 f 0.6651 3.859; 32768 256 4 c 1.1484 9.051;"
+    "32768 256 4 f 2.3864 16.630; 32768 256 6 c 1.6707 17.104; 32768 256 6 f 3.4540 30.358;"
+    "65536 32 1 c 0.1019 0.514; 65536 32 1 f 0.1997 1.059; 65536 32 4 c 0.6666 3.218;"
+    "65536 32 4 f 0.6451 4.840; 65536 32 6 c 1.2841 6.345; 65536 32 6 f 0.9062 7.769;"
+    "65536 64 1 c 0.1536 0.686; 65536 64 1 f 0.3507 1.964; 65536 64 4 c 0.5990 4.970;"
+    "65536 64 4 f 1.2145 8.309; 65536 64 6 c 0.8571 8.773; 65536 64 6 f 1.7280 14.956;"
+    "65536 128 1 c 0.2627 1.217; 65536 128 1 f 0.6661 3.844; 65536 128 4 c 1.1459 9.765;"
+    "65536 128 4 f 2.4433 16.648; 65536 128 6 c 1.6451 17.098; 65536 128 6 f 3.4186 30.087;"
+    "65536 256 1 c 0.4844 2.359; 65536 256 1 f 1.2861 7.639; 65536 256 4 c 2.2477 17.669;"
+    "65536 256 4 f 4.7145 33.167; 65536 256 6 c 3.2748 34.414; 65536 256 6 f 6.8444 60.811;"
+    "131072 32 1 c 0.1536 0.781; 131072 32 1 f 0.3533 1.988; 131072 32 4 c 1.2800 6.234;"
+    "131072 32 4 f 1.2298 9.547; 131072 32 6 c 2.5185 11.820; 131072 32 6 f 1.7418 15.075;"
+    "131072 64 1 c 0.2642 1.216; 131072 64 1 f 0.6656 3.829; 131072 64 4 c 1.1469 9.641;"
+    "131072 64 4 f 2.3700 16.430; 131072 64 6 c 1.6476 17.166; 131072 64 6 f 3.3756 30.119;"
+    "131072 128 1 c 0.4782 2.322; 131072 128 1 f 1.2969 7.608; 131072 128 4 c 2.2441 17.495;"
+    "131072 128 4 f 4.7995 33.178; 131072 128 6 c 3.2384 34.168; 131072 128 6 f 6.7779 60.348;"
+    "131072 256 1 c 0.9185 4.545; 131072 256 1 f 2.5313 13.859; 131072 256 4 c 4.4544 35.296;"
+    "131072 256 4 f 9.3507 66.198; 131072 256 6 c 6.4794 68.713;"
+    "131072 256 6 f 13.5434 124.088;"
+)
+
+
+def _a100_grid():
+    table = {}
+    for item in "".join(A100_GRID).split(";"):
+        if item.strip():
+            n, c, m, par, fwd, both = item.split()
+            table[(int(n), int(c), int(m), "full" if par == "f" else "canonical")] = (
+                float(fwd), float(both))
+    return table
+
+
+def _graph_step(torch, step, check):
+    """Capture `step` in a HIP graph; replay it three times, each checked
+    bitwise against `check` (the eager result), with eager work between."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(outs, check):
+            if not torch.equal(got, want):
+                raise RuntimeError("graph replay differs from the eager step")
+        step()                                  # eager work between replays
+    return graph
+
+
+def _replay_ms(torch, graph, samples=20):
+    import statistics
+    for _ in range(3):
+        graph.replay()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(samples + 1)]
+    torch.cuda.synchronize()
+    events[0].record()
+    for i in range(samples):
+        graph.replay()
+        events[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(events[i].elapsed_time(events[i + 1]) for i in range(samples))
+
+
+def grid_main(args):
+    """configs[2] (and configs[1]): forward and forward + full VJP of every
+    (N, C, m_max, parity) point, each step captured in a HIP graph and timed
+    as the median of 20 replays; kernel times from eager steps."""
+    import torch
+    from ictc_o2_hp import TensorProduct, _native
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    device = torch.device("cuda:0")
+    _native.library()
+    a100 = _a100_grid()
+    points = sorted(a100) + [(6400, 128, 6, "full")]
+    records = []
+    for n, c, m, parity in points:
+        torch.manual_seed(34527)
+        module = TensorProduct(c, m, parity=parity).to(device)
+        width, pw = module.representation_dimension, module.weight.numel()
+        gen = torch.Generator(device=device).manual_seed(78211)
+        x = torch.randn((n, width), device=device, generator=gen).requires_grad_()
+        y = torch.randn((n, width), device=device, generator=gen).requires_grad_()
+        cot = torch.ones((n, width), device=device)
+        params = (x, y, module.weight)
+
+        def both():
+            return torch.autograd.grad(module(x, y), params, cot)
+
+        def forward():
+            with torch.no_grad():
+                return (module(x, y),)
+
+        eager_both, eager_fwd = both(), forward()
+        g_both = _graph_step(torch, both, eager_both)
+        g_fwd = _graph_step(torch, forward, eager_fwd)
+        both_ms, fwd_ms = _replay_ms(torch, g_both), _replay_ms(torch, g_fwd)
+        _, _, kinds, _ = _timed_steps(torch, both, 5, 1)
+        kf = kinds["tp_forward"][0] / max(1, kinds["tp_forward"][1])
+        kb = kinds["tp_backward"][0] / max(1, kinds["tp_backward"][1])
+        alg = 4.0 * (8.0 * n * width + 3.0 * pw)
+        ref = a100.get((n, c, m, parity))
+        rec = {"rows": n, "channels": c, "m_max": m, "parity": parity, "width": width,
+               "fwd_ms": fwd_ms, "fwd_vjp_ms": both_ms, "rows_per_s": n / (both_ms * 1e-3),
+               "step_GBps": alg / (both_ms * 1e-3) / 1e9,
+               "kernel_fwd_ms": kf, "kernel_bwd_ms": kb,
+               "kernel_fwd_GBps": 4.0 * (3.0 * n * width + pw) / (kf * 1e-3) / 1e9,
+               "kernel_bwd_GBps": 4.0 * (5.0 * n * width + 2.0 * pw) / (kb * 1e-3) / 1e9,
+               "a100_fwd_ms": ref[0] if ref else None, "a100_fwd_vjp_ms": ref[1] if ref else None,
+               "speedup_fwd_vjp": (ref[1] / both_ms) if ref else None}
+        records.append(rec)
+        print(json.dumps(rec), flush=True)
+        del g_both, g_fwd, eager_both, eager_fwd, x, y, cot, module
+        torch.cuda.empty_cache()
+    if args.grid_out:
+        Path(args.grid_out).write_text(json.dumps(records, indent=1))
+
+
 def main():
     args = _args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         raise SystemExit(2)
+    if args.workload == "grid":
+        return grid_main(args)
     if args.workload != "tp":
         (radial_main if args.workload == "radial" else uvu_main)(args)
         return _copy_probe(args)
