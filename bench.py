@@ -56,6 +56,9 @@ def _args():
                    help="after the run, copy 512 MiB 3 times with an elementwise kernel "
                         "(reference traffic for HBM counter calibration)")
     p.add_argument("--edges", type=int, default=1048576, help="radial workload: edges")
+    p.add_argument("--torch-gather", action="store_true",
+                   help="radial workload: gather node features with torch indexing (atomic "
+                        "scatter-add backward) instead of the fused left_index gather")
     p.add_argument("--uvu-rows", type=int, default=16384,
                    help="uvu workload: rows (65536 needs 524 GB of per-row weights)")
     return p.parse_args()
@@ -143,9 +146,12 @@ def _timed_steps(torch, step, steps, warmup):
     return events[0].elapsed_time(events[-1]) / steps, wall_ms / steps, kinds, samples
 
 
-def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidden=64):
+def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidden=64,
+                  fused_gather=True):
     """gather x from nodes, Bessel(8) radial features with a cosine
-    cutoff -> MLP 8->64->64 (SiLU) -> fused final affine + V=1 uvu product."""
+    cutoff -> MLP 8->64->64 (SiLU) -> fused final affine + V=1 uvu product.
+    ``fused_gather``: the radial kernels read node rows through ``left_index``
+    (table gradient summed in a fixed order); otherwise ``node_feats[src]``."""
     import math
     from ictc_o2_hp import RadialUvuTensorProduct, UvuTensorProduct
 
@@ -161,6 +167,8 @@ def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidde
             self.radial = RadialUvuTensorProduct(tp, radial_out)
 
         def forward(self, node_feats, src, basis, angular):
+            if fused_gather:
+                return self.radial(node_feats, angular, self.trunk(basis), left_index=src)
             return self.radial(node_feats[src], angular, self.trunk(basis))
 
     chain = Chain().to(device)
@@ -221,7 +229,8 @@ def radial_main(args):
     _native.library()
     torch.manual_seed(2024)
     edges = args.edges
-    chain, tp, node_feats, src, basis, angular = _radial_chain(torch, device, edges)
+    chain, tp, node_feats, src, basis, angular = _radial_chain(
+        torch, device, edges, fused_gather=not args.torch_gather)
     run = chain if args.no_compile else torch.compile(chain, fullgraph=True, dynamic=False)
     params = [node_feats] + list(chain.parameters())
     cot = torch.ones((edges, tp.input1_dimension), device=device)
@@ -248,6 +257,7 @@ def radial_main(args):
                 "affine, ones cotangent",
         "config": {"workload": f"RadialUvuTensorProduct C64 m4 canonical E={edges} "
                                "(gather from 65536 nodes, MLP 8->64->64 SiLU) fwd+full VJP",
+                   "gather": "torch indexing" if args.torch_gather else "fused left_index",
                    "edges": edges, "channels": 64, "m_max": 4, "hidden": hidden,
                    "weights_per_edge": pw, "compiled": not args.no_compile},
         "ms_per_step_median": median, "ms_per_step_iqr": iqr,

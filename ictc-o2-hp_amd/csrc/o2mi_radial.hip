@@ -93,7 +93,21 @@ Args make_args(const o2mi_radial_plan* p, int64_t n, const float* x, const float
   a.alpha = alpha;
   a.bias = bias;
   a.coef = coef;
+  a.xindex = nullptr;
+  a.x_rows = n;
   return a;
+}
+
+// Gathered first input: x is a table of `table_rows` rows read through
+// `index`; the kernels address it with one 32-bit buffer descriptor.
+int gather_args(const o2mi_radial_plan* p, Args* a, int64_t table_rows, const int64_t* index) {
+  if (table_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "table_rows must be non-negative");
+  if (table_rows * p->W1 * 4 >= ((int64_t)1 << 31))
+    return fail(O2MI_ERR_UNSUPPORTED, "gathered first-input table must be below 2 GiB");
+  if (!index && a->n > 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "index is NULL");
+  a->xindex = index;
+  a->x_rows = table_rows;
+  return O2MI_OK;
 }
 
 int check_inputs(const float* x, const float* y, const float* hidden, const float* alpha,
@@ -112,6 +126,85 @@ int check_inputs(const float* x, const float* y, const float* hidden, const floa
 }  // namespace o2mi
 
 using namespace o2mi::radial;
+
+namespace {
+
+int radial_forward(const o2mi_radial_plan* plan, const Args& a, float* out, void* stream) {
+  if (a.n == 0) return O2MI_OK;
+  if (int st = check_inputs(a.x, a.y, a.hidden, a.alpha, a.bias, a.coef)) return st;
+  if (!aligned16(out)) return fail(O2MI_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_FORWARD);
+  const hipError_t err = plan->set->forward(a, out, s);
+  if (timing) o2mi_timing_end(s, &timed);
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial forward launch");
+}
+
+int radial_backward(const o2mi_radial_plan* plan, const Args& a, const float* grad_output,
+                    float* gx, float* gy, float* ghidden, float* galpha, float* gbias,
+                    void* workspace, size_t workspace_bytes, int needed, void* stream) {
+  const int64_t n_rows = a.n;
+  const float* bias = a.bias;
+  if (needed & ~31) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1..16");
+  if (needed & 16 && !bias)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "bias gradient requested without a bias");
+  if (((needed & 8) && !galpha) || ((needed & 16) && !gbias))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested affine gradient");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows = (int64_t)plan->set->paths * plan->C;
+  if (n_rows == 0) {
+    // No edges: the affine adjoints are zero, the other roles are empty.
+    if (needed & 8) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows * plan->H)), dim3(256),
+                                       0, s, galpha, rows * plan->H);
+    if (needed & 16) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows)), dim3(256), 0, s,
+                                        gbias, rows);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial zero fill");
+  }
+  if (int st = check_inputs(a.x, a.y, a.hidden, a.alpha, a.bias, a.coef)) return st;
+  if (!grad_output || !aligned16(grad_output))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "grad_output must be a 16-byte aligned pointer");
+  if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy) ||
+      ((needed & 4) && !aligned16(ghidden)))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
+  if ((needed & 8) && !aligned16(galpha))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "galpha must be 16-byte aligned");
+  if (needed & 7) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_BACKWARD);
+    const hipError_t err = plan->set->backward(a, grad_output, gx, gy, ghidden, needed & 7, s);
+    if (timing) o2mi_timing_end(s, &timed);
+    if (err != hipSuccess) return fail_hip(err, "radial backward launch");
+  }
+  if (needed & 24) {
+    int64_t per = 0;
+    int slices = 0;
+    slicing(plan, n_rows, &per, &slices);
+    const size_t need = (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+      return fail(O2MI_ERR_WORKSPACE,
+                  "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
+    float* part_alpha = static_cast<float*>(workspace);
+    float* part_bias = part_alpha + (int64_t)slices * rows * plan->H;
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_WEIGHT);
+    hipError_t err = plan->set->weight(a, grad_output, per, slices, part_alpha, part_bias, s);
+    if (timing) o2mi_timing_end(s, &timed);
+    if (err != hipSuccess) return fail_hip(err, "radial weight launch");
+    if (needed & 8)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows * plan->H)), dim3(256), 0, s,
+                         part_alpha, slices, rows * plan->H, galpha);
+    if (needed & 16)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows)), dim3(256), 0, s, part_bias,
+                         slices, rows, gbias);
+    err = hipGetLastError();
+    if (err != hipSuccess) return fail_hip(err, "radial slice sum launch");
+  }
+  return O2MI_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -151,16 +244,19 @@ int o2mi_radial_forward_f32(const o2mi_radial_plan* plan, const float* x, const 
                             const float* coefficients, float* out, int64_t n_rows,
                             void* stream) {
   if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
-  if (n_rows == 0) return O2MI_OK;
-  if (int st = check_inputs(x, y, hidden, alpha, bias, coefficients)) return st;
-  if (!aligned16(out)) return fail(O2MI_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
   const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  O2miTimed timed;
-  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_FORWARD);
-  const hipError_t err = plan->set->forward(a, out, s);
-  if (timing) o2mi_timing_end(s, &timed);
-  return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial forward launch");
+  return radial_forward(plan, a, out, stream);
+}
+
+int o2mi_radial_forward_gather_f32(const o2mi_radial_plan* plan, const float* x_table,
+                                   int64_t table_rows, const int64_t* index, const float* y,
+                                   const float* hidden, const float* alpha, const float* bias,
+                                   const float* coefficients, float* out, int64_t n_rows,
+                                   void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  Args a = make_args(plan, n_rows, x_table, y, hidden, alpha, bias, coefficients);
+  if (int st = gather_args(plan, &a, table_rows, index)) return st;
+  return radial_forward(plan, a, out, stream);
 }
 
 size_t o2mi_radial_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
@@ -180,63 +276,23 @@ int o2mi_radial_backward_f32(const o2mi_radial_plan* plan, const float* x, const
                              void* workspace, size_t workspace_bytes, int64_t n_rows, int needed,
                              void* stream) {
   if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
-  if (needed & ~31) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1..16");
-  if (needed & 16 && !bias)
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "bias gradient requested without a bias");
-  if (((needed & 8) && !galpha) || ((needed & 16) && !gbias))
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested affine gradient");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t rows = (int64_t)plan->set->paths * plan->C;
-  if (n_rows == 0) {
-    // No edges: the affine adjoints are zero, the other roles are empty.
-    if (needed & 8) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows * plan->H)), dim3(256),
-                                       0, s, galpha, rows * plan->H);
-    if (needed & 16) hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(rows)), dim3(256), 0, s,
-                                        gbias, rows);
-    const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? O2MI_OK : fail_hip(err, "radial zero fill");
-  }
-  if (int st = check_inputs(x, y, hidden, alpha, bias, coefficients)) return st;
-  if (!grad_output || !aligned16(grad_output))
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "grad_output must be a 16-byte aligned pointer");
-  if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy) ||
-      ((needed & 4) && !aligned16(ghidden)))
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
-  if ((needed & 8) && !aligned16(galpha))
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "galpha must be 16-byte aligned");
   const Args a = make_args(plan, n_rows, x, y, hidden, alpha, bias, coefficients);
-  if (needed & 7) {
-    O2miTimed timed;
-    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_BACKWARD);
-    const hipError_t err = plan->set->backward(a, grad_output, gx, gy, ghidden, needed & 7, s);
-    if (timing) o2mi_timing_end(s, &timed);
-    if (err != hipSuccess) return fail_hip(err, "radial backward launch");
-  }
-  if (needed & 24) {
-    int64_t per = 0;
-    int slices = 0;
-    slicing(plan, n_rows, &per, &slices);
-    const size_t need = (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
-    if (!workspace || workspace_bytes < need || !aligned16(workspace))
-      return fail(O2MI_ERR_WORKSPACE,
-                  "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
-    float* part_alpha = static_cast<float*>(workspace);
-    float* part_bias = part_alpha + (int64_t)slices * rows * plan->H;
-    O2miTimed timed;
-    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_WEIGHT);
-    hipError_t err = plan->set->weight(a, grad_output, per, slices, part_alpha, part_bias, s);
-    if (timing) o2mi_timing_end(s, &timed);
-    if (err != hipSuccess) return fail_hip(err, "radial weight launch");
-    if (needed & 8)
-      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows * plan->H)), dim3(256), 0, s,
-                         part_alpha, slices, rows * plan->H, galpha);
-    if (needed & 16)
-      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(rows)), dim3(256), 0, s, part_bias,
-                         slices, rows, gbias);
-    err = hipGetLastError();
-    if (err != hipSuccess) return fail_hip(err, "radial slice sum launch");
-  }
-  return O2MI_OK;
+  return radial_backward(plan, a, grad_output, gx, gy, ghidden, galpha, gbias, workspace,
+                         workspace_bytes, needed, stream);
+}
+
+int o2mi_radial_backward_gather_f32(const o2mi_radial_plan* plan, const float* x_table,
+                                    int64_t table_rows, const int64_t* index, const float* y,
+                                    const float* hidden, const float* alpha, const float* bias,
+                                    const float* coefficients, const float* grad_output,
+                                    float* gx_edges, float* gy, float* ghidden, float* galpha,
+                                    float* gbias, void* workspace, size_t workspace_bytes,
+                                    int64_t n_rows, int needed, void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  Args a = make_args(plan, n_rows, x_table, y, hidden, alpha, bias, coefficients);
+  if (int st = gather_args(plan, &a, table_rows, index)) return st;
+  return radial_backward(plan, a, grad_output, gx_edges, gy, ghidden, galpha, gbias, workspace,
+                         workspace_bytes, needed, stream);
 }
 
 }  // extern "C"

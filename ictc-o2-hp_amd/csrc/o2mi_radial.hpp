@@ -108,6 +108,11 @@ struct Args {
   const float* alpha;  // [P*C, H]
   const float* bias;   // [P*C] or null
   const float* coef;   // [P][2][2][2]
+  // Gathered first input: null, x row e for edge e; else x is a table of
+  // x_rows rows (x_rows * W1 * 4 < 2^31 bytes) and edge e reads row
+  // xindex[e]; an index outside [0, x_rows) reads zeros.
+  const int64_t* xindex;
+  int64_t x_rows;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int64_t row0,
@@ -115,6 +120,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, i
   const int64_t valid = rows < 0 ? 0 : rows;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base) + row0 * width, 0,
                                            (int)(valid * width * 4), kRsrcFlags);
+}
+
+// First-input descriptor of the edges [e0, e0 + rows): those rows of x, or
+// the whole node table when the first input is gathered.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const Args& a, int64_t e0,
+                                                         int64_t rows) {
+  return a.xindex ? rows_rsrc(a.x, 0, a.W1, a.x_rows) : rows_rsrc(a.x, e0, a.W1, rows);
+}
+
+// Byte offset of edge e0 + j's first-input row inside x_rsrc(a, e0, rows)
+// (kIdle past the last edge or for an index outside the table).
+__device__ __forceinline__ uint32_t x_row_off(const Args& a, int64_t e0, int64_t rows, int j) {
+  if (!a.xindex) return (uint32_t)(j * a.W1) * 4u;
+  if (j >= rows) return kIdle;
+  const int64_t id = a.xindex[e0 + j];
+  return (id >= 0 && id < a.x_rows) ? (uint32_t)id * (uint32_t)a.W1 * 4u : kIdle;
 }
 
 __device__ __forceinline__ float ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
@@ -242,11 +263,12 @@ __global__ __launch_bounds__(kThreads, 1) void radial_forward_kernel(Args a, flo
   const int g = lane >> 4, j = lane & 15;
   const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
-  const auto rx = rows_rsrc(a.x, e0, a.W1, rows);
+  const auto rx = x_rsrc(a, e0, rows);
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
   const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
   const auto ro = rows_rsrc(out, e0, a.W1, rows);
-  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (out)
+  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
 
   for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
   float hid[KH];
@@ -269,7 +291,7 @@ __global__ __launch_bounds__(kThreads, 1) void radial_forward_kernel(Args a, flo
     asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off));
     const float* cf_tile = s_mem + coef_off;
     float xv[4 * NC];
-    load_row<Plan>(rx, xrow, a.C, u, xv);
+    load_row<Plan>(rx, xsrc, a.C, u, xv);
     float ov[4 * NC];
     static_for<4 * NC>([&](auto ic) { ov[decltype(ic)::value] = 0.f; });
     static_for<P>([&](auto pc) {
@@ -316,11 +338,12 @@ __global__ __launch_bounds__(kThreads, 1) void radial_backward_kernel(Args a, co
   const int g = lane >> 4, j = lane & 15;
   const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
-  const auto rx = rows_rsrc(a.x, e0, a.W1, rows);
+  const auto rx = x_rsrc(a, e0, rows);
   const auto rg = rows_rsrc(gout, e0, a.W1, rows);
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
   const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
-  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (g, dx)
+  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
   // Every role is computed; a role that is not requested gets a zero-size
   // store descriptor.  Branches on the roles cost more registers (the
   // compiler duplicates the channel loop) than the rarely skipped work.
@@ -350,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 1) void radial_backward_kernel(Args a, co
     asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off));
     const float* cf_tile = s_mem + coef_off;
     float xv[4 * NC], gv[4 * NC], dxv[4 * NC];
-    load_row<Plan>(rx, xrow, a.C, u, xv);
+    load_row<Plan>(rx, xsrc, a.C, u, xv);
     load_row<Plan>(rg, xrow, a.C, u, gv);
     static_for<4 * NC>([&](auto ic) { dxv[decltype(ic)::value] = 0.f; });
     static_for<P>([&](auto pc) {
@@ -445,27 +468,59 @@ __device__ __forceinline__ int tile_x_offset(int idx_in_edge, int C, int u0) {
   return off;
 }
 
+// Gathered first input: lane L of every wave holds the table row of edge
+// t0 + (L % 32) of a tile (-1 past the end).  Loaded one tile ahead of its use,
+// so the x loads of a tile never wait on a dependent index load.
+__device__ __forceinline__ int64_t tile_rows(const Args& a, int64_t t0, int64_t t_end) {
+  if (!a.xindex) return 0;
+  const int64_t e = t0 + (threadIdx.x & 31);
+  return e < t_end ? a.xindex[e] : -1;
+}
+
+// Byte offset of tile edge `edge`'s table row (kIdle if outside the table),
+// taken from the lane that loaded it.
+__device__ __forceinline__ uint32_t tile_row_off(const Args& a, int64_t rows_of_tile, int edge) {
+  const int lo = __shfl((int)(uint32_t)(uint64_t)rows_of_tile, edge);
+  const int hi = __shfl((int)(uint32_t)((uint64_t)rows_of_tile >> 32), edge);
+  const int64_t id = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  return (id >= 0 && id < a.x_rows) ? (uint32_t)id * (uint32_t)a.W1 * 4u : kIdle;
+}
+
 template <class Plan, int KH>
 __device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH>& pf, const Args& a,
                                              const float* gout, int64_t t0, int64_t t_end,
-                                             int u0) {
+                                             int u0, int64_t rows_of_tile) {
   using T = WTile<Plan, KH>;
   constexpr int XE = 16 * Plan::kComps1;
   const int64_t rows = t_end - t0 < kWeightEdges ? t_end - t0 : kWeightEdges;
-  const auto rx = rows_rsrc(a.x, t0, a.W1, rows);
+  const auto rx = x_rsrc(a, t0, rows);
   const auto rg = rows_rsrc(gout, t0, a.W1, rows);
   const auto ry = rows_rsrc(a.y, t0, a.W2, rows);
   const auto rh = rows_rsrc(a.hidden, t0, a.H, rows);
+  // Offsets first (the table rows come from other lanes), then every load, so
+  // no load of the tile waits behind another.
+  uint32_t voff[T::kXPer], xoff[T::kXPer];
   static_for<T::kXPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     const int idx = threadIdx.x + k * kThreads;
-    uint32_t voff = kIdle;
+    voff[k] = xoff[k] = kIdle;
     if (idx < kWeightEdges * XE) {
       const int edge = idx / XE;
-      voff = (uint32_t)(edge * a.W1 + tile_x_offset<Plan>(idx - edge * XE, a.C, u0)) * 4u;
+      const uint32_t col = (uint32_t)tile_x_offset<Plan>(idx - edge * XE, a.C, u0) * 4u;
+      voff[k] = (uint32_t)(edge * a.W1) * 4u + col;
+      if (a.xindex) {
+        const uint32_t row = edge < rows ? tile_row_off(a, rows_of_tile, edge) : kIdle;
+        xoff[k] = row == kIdle ? kIdle : row + col;
+      } else {
+        xoff[k] = voff[k];
+      }
     }
-    pf.x[k] = ld1(rx, voff);
-    pf.g[k] = ld1(rg, voff);
+  });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<T::kXPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    pf.x[k] = ld1(rx, xoff[k]);
+    pf.g[k] = ld1(rg, voff[k]);
   });
   static_for<T::kYPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
@@ -545,13 +600,18 @@ __global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
 
   WPrefetch<Plan, KH> pf;
   if (tiles > 0) {
-    weight_fetch<Plan, KH>(pf, a, gout, begin, end, u0);
+    weight_fetch<Plan, KH>(pf, a, gout, begin, end, u0, tile_rows(a, begin, end));
     weight_commit<Plan, KH>(pf, s_tile);
   }
+  int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
   __syncthreads();
   for (int t = 0; t < tiles; ++t) {
     const bool more = t + 1 < tiles;
-    if (more) weight_fetch<Plan, KH>(pf, a, gout, begin + (int64_t)(t + 1) * kWeightEdges, end, u0);
+    if (more) {
+      const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
+      weight_fetch<Plan, KH>(pf, a, gout, t1, end, u0, next_rows);
+      next_rows = tile_rows(a, t1 + kWeightEdges, end);
+    }
     const float* buf = s_tile + (t & 1) * T::kFloats;
     const float* sx = buf;
     const float* sg = buf + T::kX;

@@ -10,7 +10,7 @@ __version__ = "0.1.6.dev0"
 __all__ = [
     "TensorProduct", "TupleTensorProduct", "ComponentMajorTensorProduct",
     "ReferenceTensorProduct", "UvuTensorProduct", "ReferenceUvuTensorProduct", "__version__",
-    "RadialUvuTensorProduct",
+    "RadialUvuTensorProduct", "gather_rows", "scatter_add_rows",
 ]
 
 
@@ -22,6 +22,9 @@ def __getattr__(name):
     if name == "RadialUvuTensorProduct":
         from .radial_uvu import RadialUvuTensorProduct
         return RadialUvuTensorProduct
+    if name in {"gather_rows", "scatter_add_rows"}:
+        from . import graph_ops
+        return getattr(graph_ops, name)
     if name in {"UvuTensorProduct", "ReferenceUvuTensorProduct"}:
         from . import uvu_o2
         return getattr(uvu_o2, name)

@@ -84,6 +84,17 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_radial_backward_f32.restype = c_int
     lib.o2mi_radial_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp,
                                              vp, c_sz, c_i64, c_int, vp]
+    lib.o2mi_radial_forward_gather_f32.restype = c_int
+    lib.o2mi_radial_forward_gather_f32.argtypes = [vp, fp, c_i64, vp, fp, fp, fp, fp, fp, fp,
+                                                   c_i64, vp]
+    lib.o2mi_radial_backward_gather_f32.restype = c_int
+    lib.o2mi_radial_backward_gather_f32.argtypes = [vp, fp, c_i64, vp, fp, fp, fp, fp, fp, fp,
+                                                    fp, fp, fp, fp, fp, vp, c_sz, c_i64, c_int,
+                                                    vp]
+    lib.o2mi_rows_gather_f32.restype = c_int
+    lib.o2mi_rows_gather_f32.argtypes = [fp, c_i64, vp, c_i64, c_i64, fp, vp]
+    lib.o2mi_rows_segment_sum_f32.restype = c_int
+    lib.o2mi_rows_segment_sum_f32.argtypes = [fp, c_i64, c_i64, vp, vp, c_i64, fp, vp]
     lib.o2mi_tp_launch_shape.restype = c_int
     lib.o2mi_tp_launch_shape.argtypes = [vp, c_i64, c_int] + [ctypes.POINTER(c_int)] * 4
     lib.o2mi_kernel_timing.restype = c_int

@@ -290,3 +290,199 @@ def _backward_backward(ctx, d_left, d_angular, d_radial, d_alpha, d_bias):
 
 
 radial_backward.register_autograd(_backward_backward, setup_context=_backward_setup)
+
+
+# ---------------------------------------------------------------------------
+# Gathered first input: edge e reads row index[e] of a node table.  The fused
+# kernels address the table directly (the gathered rows are never
+# materialised); the table's adjoint is the per-edge adjoint summed onto table
+# rows in a fixed order (graph_ops).  Not in the reference, which gathers with
+# torch indexing outside its radial chain (docs/RADIAL.md:97-99).
+
+_TABLE_BYTES_LIMIT = 1 << 31
+
+
+def _gather_fused(table, metadata_id, hidden):
+    plan = fused_plan(metadata_id, hidden)
+    if plan is None or table.numel() * 4 >= _TABLE_BYTES_LIMIT or table.shape[0] == 0:
+        return None
+    return plan
+
+
+def _gather_forward_impl(table, index, angular, radial, alpha, bias, info, coefficients,
+                         first_order, second_order, metadata_id, has_bias):
+    from . import graph_ops
+    _check_operands(table, angular, radial, alpha, coefficients)
+    rows = index.shape[0]
+    result = table.new_empty((rows, table.shape[1]))
+    if rows == 0:
+        return result
+    plan = _gather_fused(table, metadata_id, radial.shape[1])
+    if plan is None:
+        left = graph_ops._gather_rows(table, index)
+        return _forward_impl(left, angular, radial, alpha, bias, info, coefficients, first_order,
+                             second_order, metadata_id, has_bias)
+    table, radial, alpha = _aligned(table), _aligned(radial), _aligned(alpha)
+    angular = angular.contiguous()
+    with torch.cuda.device(table.device):
+        _native.check(_native.library().o2mi_radial_forward_gather_f32(
+            plan, table.data_ptr(), table.shape[0], index.data_ptr(), angular.data_ptr(),
+            radial.data_ptr(), alpha.data_ptr(), _ptr(bias) if has_bias else None,
+            coefficients.data_ptr(), result.data_ptr(), rows, _stream(table.device)),
+            "o2mi_radial_forward_gather_f32")
+    return result
+
+
+def _gather_backward_impl(table, index, angular, radial, alpha, bias, grad_output, info,
+                          coefficients, first_order, second_order, metadata_id, has_bias, needed):
+    from . import graph_ops
+    _check_operands(table, angular, radial, alpha, coefficients, grad_output)
+    rows = index.shape[0]
+    plan = _gather_fused(table, metadata_id, radial.shape[1])
+    if plan is None or rows == 0:
+        left = graph_ops._gather_rows(table, index)
+        gx, gy, gr, ga, gb = _backward_impl(left, angular, radial, alpha, bias, grad_output,
+                                            info, coefficients, first_order, second_order,
+                                            metadata_id, has_bias, needed)
+    else:
+        has_bias = has_bias and bias.numel() > 0
+        if not has_bias:
+            needed &= ~16
+        width = table.shape[1]
+        gx = table.new_empty((rows, width)) if needed & 1 else table.new_empty(0)
+        gy = torch.empty_like(angular) if needed & 2 else angular.new_empty(0)
+        gr = torch.empty_like(radial) if needed & 4 else radial.new_empty(0)
+        ga = torch.empty_like(alpha) if needed & 8 else alpha.new_empty(0)
+        gb = torch.empty_like(bias) if needed & 16 else bias.new_empty(0)
+        if needed:
+            lib = _native.library()
+            table, radial, alpha = _aligned(table), _aligned(radial), _aligned(alpha)
+            grad_output = _aligned(grad_output)
+            angular = angular.contiguous()
+            ws_bytes = int(lib.o2mi_radial_backward_workspace_bytes(plan, rows, needed))
+            workspace = torch.empty(max(4, (ws_bytes + 3) // 4), dtype=torch.float32,
+                                    device=table.device)
+            with torch.cuda.device(table.device):
+                _native.check(lib.o2mi_radial_backward_gather_f32(
+                    plan, table.data_ptr(), table.shape[0], index.data_ptr(), angular.data_ptr(),
+                    radial.data_ptr(), alpha.data_ptr(), _ptr(bias) if has_bias else None,
+                    coefficients.data_ptr(), grad_output.data_ptr(), _ptr(gx), _ptr(gy),
+                    _ptr(gr), _ptr(ga), _ptr(gb), workspace.data_ptr(), ws_bytes, rows, needed,
+                    _stream(table.device)), "o2mi_radial_backward_gather_f32")
+    if needed & 1:
+        order, offsets = graph_ops.csr_runs(index, table.shape[0])
+        g_table = graph_ops.segment_sum_native(gx, order, offsets, table.shape[0])
+    else:
+        g_table = table.new_empty(0)
+    return g_table, gy, gr, ga, gb
+
+
+@torch.library.custom_op(NAMESPACE + "::radial_gather_forward", mutates_args=())
+def radial_gather_forward(table: torch.Tensor, index: torch.Tensor, angular: torch.Tensor,
+                          radial: torch.Tensor, alpha: torch.Tensor, bias: torch.Tensor,
+                          info: torch.Tensor, coefficients: torch.Tensor,
+                          first_order: torch.Tensor, second_order: torch.Tensor,
+                          metadata_id: int, has_bias: bool) -> torch.Tensor:
+    return _gather_forward_impl(table, index, angular, radial, alpha, bias, info, coefficients,
+                                first_order, second_order, metadata_id, has_bias)
+
+
+@radial_gather_forward.register_fake
+def _radial_gather_forward_fake(table, index, angular, radial, alpha, bias, info, coefficients,
+                                first_order, second_order, metadata_id, has_bias):
+    return table.new_empty((index.shape[0], table.shape[1]))
+
+
+@torch.library.custom_op(NAMESPACE + "::radial_gather_backward", mutates_args=())
+def radial_gather_backward(table: torch.Tensor, index: torch.Tensor, angular: torch.Tensor,
+                           radial: torch.Tensor, alpha: torch.Tensor, bias: torch.Tensor,
+                           grad_output: torch.Tensor, info: torch.Tensor,
+                           coefficients: torch.Tensor, first_order: torch.Tensor,
+                           second_order: torch.Tensor, metadata_id: int, has_bias: bool,
+                           needed: int = 31
+                           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                      torch.Tensor]:
+    return _gather_backward_impl(table, index, angular, radial, alpha, bias,
+                                 grad_output.contiguous(), info, coefficients, first_order,
+                                 second_order, metadata_id, has_bias, needed)
+
+
+@radial_gather_backward.register_fake
+def _radial_gather_backward_fake(table, index, angular, radial, alpha, bias, grad_output, info,
+                                 coefficients, first_order, second_order, metadata_id, has_bias,
+                                 needed=31):
+    if not (has_bias and bias.numel() > 0):
+        needed &= ~16
+    return tuple(torch.empty_like(v) if needed & (1 << i) else v.new_empty(0)
+                 for i, v in enumerate((table, angular, radial, alpha, bias)))
+
+
+def _gather_forward_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[:10])
+    ctx.metadata_id, ctx.has_bias = inputs[10], inputs[11]
+
+
+def _gather_forward_backward(ctx, grad_output):
+    (table, index, angular, radial, alpha, bias, info, coefficients, first_order,
+     second_order) = ctx.saved_tensors
+    needs = ctx.needs_input_grad
+    roles = uvu_ops.required_gradients((table, angular, radial, alpha, bias),
+                                       (needs[0], needs[2], needs[3], needs[4], needs[5]))
+    grads = radial_gather_backward(table, index, angular, radial, alpha, bias,
+                                   grad_output.contiguous(), info, coefficients, first_order,
+                                   second_order, ctx.metadata_id, ctx.has_bias, _mask(roles))
+    g = [gr if r else None for gr, r in zip(grads, roles)]
+    return (g[0], None, g[1], g[2], g[3], g[4], None, None, None, None, None, None)
+
+
+radial_gather_forward.register_autograd(_gather_forward_backward,
+                                        setup_context=_gather_forward_setup)
+
+
+def _gather_backward_setup(ctx, inputs, output):
+    (table, index, angular, radial, alpha, bias, grad_output, info, coefficients, first_order,
+     second_order, metadata_id, has_bias, needed) = inputs
+    ctx.save_for_backward(table, index, angular, radial, alpha, bias, grad_output, info,
+                          coefficients, first_order, second_order)
+    ctx.metadata_id, ctx.has_bias, ctx.needed = metadata_id, has_bias, needed
+    ctx.set_materialize_grads(False)
+
+
+def _gather_backward_backward(ctx, d_table, d_angular, d_radial, d_alpha, d_bias):
+    """Second order through the differentiable composition: the table adjoint
+    is scatter_add(first-order input adjoint of gather(table)), and gather and
+    scatter_add are each other's adjoints, so the radial op's own second order
+    (``_backward_backward``) supplies every term."""
+    from . import graph_ops
+    (table, index, angular, radial, alpha, bias, grad_output, info, coefficients, first_order,
+     second_order) = ctx.saved_tensors
+    cot = (d_table, d_angular, d_radial, d_alpha, d_bias)
+    selected = [i for i, c in enumerate(cot) if c is not None and c.numel()]
+    needs = ctx.needs_input_grad
+    positions = (0, 2, 3, 4, 5, 6)          # table, angular, radial, alpha, bias, grad_output
+    if not selected or not any(needs[p] for p in positions):
+        return (None,) * 14
+    with torch.enable_grad():
+        leaves = [v.detach().requires_grad_(bool(needs[p]))
+                  for v, p in zip((table, angular, radial, alpha, bias, grad_output), positions)]
+        t, y, r, a, b, go = leaves
+        left = graph_ops._gather_rows(t, index)
+        mask = sum(1 << i for i in selected)
+        grads = radial_backward(left, y, r, a, b, a.new_empty(0), go, info, coefficients,
+                                first_order, second_order, ctx.metadata_id, ctx.has_bias, mask)
+        outs = list(grads)
+        if mask & 1:
+            outs[0] = graph_ops._scatter_add_rows(grads[0], index, table.shape[0])
+        wrt = [v for v in leaves if v.requires_grad]
+        got = torch.autograd.grad([outs[i] for i in selected], wrt,
+                                  [cot[i].contiguous() for i in selected], allow_unused=True)
+    it = iter(got)
+    mapped = [next(it) if v.requires_grad else None for v in leaves]
+    result = [None] * 14
+    for value, p in zip(mapped, positions):
+        result[p] = value
+    return tuple(result)
+
+
+radial_gather_backward.register_autograd(_gather_backward_backward,
+                                         setup_context=_gather_backward_setup)

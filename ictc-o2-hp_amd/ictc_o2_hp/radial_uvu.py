@@ -7,6 +7,14 @@ V=1 O(2) uvu product (Parity-LRX/ICTC-O2-HP ``radial_uvu.py:10-66``).
 kernels generate each edge's weights on the matrix cores and consume them in
 registers; other dtypes, devices and a ``ReferenceUvuTensorProduct`` use the
 original differentiable composition.
+
+``forward(table, angular, radial_hidden, left_index=index)`` (an extension:
+the reference gathers outside its chain, docs/RADIAL.md:97-99) equals
+``tp(table[index], angular, radial_out(radial_hidden))`` for a node table
+``[nodes, input1_dimension]`` and int64/int32 edge index ``[edges]``: the
+fused kernels read the table rows directly, and the table's gradient sums the
+edge adjoints onto table rows in a fixed order (``graph_ops``), so it is
+bitwise reproducible.  An index outside ``[0, nodes)`` reads a zero row.
 """
 from __future__ import annotations
 
@@ -41,7 +49,9 @@ class RadialUvuTensorProduct(torch.nn.Module):
             radial_ops.register_structure(tp._kernel_metadata_id, tp.channels, tp.m_max,
                                           tp.parity, tp.m_max_in2, tp.parity_in2)
 
-    def forward(self, left, angular, radial_hidden):
+    def forward(self, left, angular, radial_hidden, *, left_index=None):
+        if left_index is not None:
+            return self._forward_gathered(left, left_index, angular, radial_hidden)
         tp = self.tp
         if left.ndim < 1 or left.shape[-1] != tp.input1_dimension:
             raise ValueError("left has the wrong final dimension")
@@ -72,3 +82,37 @@ class RadialUvuTensorProduct(torch.nn.Module):
             tp._kernel_metadata_id, bias is not None,
             torch.is_grad_enabled() and (left.requires_grad or angular.requires_grad))
         return result.reshape(*left.shape[:-1], tp.representation_dimension)
+
+    def _forward_gathered(self, table, index, angular, radial_hidden):
+        tp = self.tp
+        if table.ndim != 2 or table.shape[-1] != tp.input1_dimension:
+            raise ValueError("with left_index, left must be a [rows, input1_dimension] table")
+        if index.ndim != 1 or index.dtype not in (torch.int64, torch.int32):
+            raise ValueError("left_index must be a 1-D int64 or int32 tensor")
+        if index.device != table.device:
+            raise ValueError("left_index must be on the table's device")
+        edges = index.shape[0]
+        if angular.shape != (edges, tp.input2_dimension):
+            raise ValueError("angular must be [len(left_index), input2_dimension]")
+        if radial_hidden.shape != (edges, self.radial_out.in_features):
+            raise ValueError("radial_hidden must be [len(left_index), radial_out.in_features]")
+        if not table.is_floating_point():
+            raise TypeError("radial uvu operands must be real floating-point tensors")
+        operands = [angular, radial_hidden, self.radial_out.weight, tp._coefficients]
+        if self.radial_out.bias is not None:
+            operands.append(self.radial_out.bias)
+        if any(v.device != table.device or v.dtype != table.dtype for v in operands):
+            raise ValueError("all operands and modules must have the same device and dtype")
+        from . import graph_ops
+        if (table.device.type != "cuda" or table.dtype != torch.float32
+                or not isinstance(tp, UvuTensorProduct)):
+            left = graph_ops.gather_rows(table, index)
+            return tp(left, angular, self.radial_out(radial_hidden))
+        from .radial_ops import radial_gather_forward
+        bias = self.radial_out.bias
+        return radial_gather_forward(
+            table.contiguous(), index.to(torch.int64).contiguous(), angular.contiguous(),
+            radial_hidden.contiguous(), self.radial_out.weight.contiguous(),
+            bias.contiguous() if bias is not None else self.radial_out.weight.new_empty(0),
+            tp._path_info, tp._coefficients, tp._first_order, tp._second_order,
+            tp._kernel_metadata_id, bias is not None)

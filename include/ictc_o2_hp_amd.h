@@ -161,6 +161,19 @@ int o2mi_radial_forward_f32(const o2mi_radial_plan *plan, const float *x, const 
                             const float *coefficients, float *out, int64_t n_rows,
                             void *stream);
 
+/* o2mi_radial_forward_f32 with a gathered first input: edge e reads row
+ * index[e] of x_table ([table_rows, W1], 16-byte aligned, below 2 GiB; an
+ * index outside [0, table_rows) reads a zero row).  Equals the reference's
+ * composition tp(x_table[index], y, radial_out(hidden)) (radial_uvu.py:50-52)
+ * without materialising the gathered rows; the node -> edge gather of a
+ * message-passing layer, which the reference leaves outside its radial chain
+ * (docs/RADIAL.md:97-99).  O2MI_ERR_UNSUPPORTED for a larger table. */
+int o2mi_radial_forward_gather_f32(const o2mi_radial_plan *plan, const float *x_table,
+                                   int64_t table_rows, const int64_t *index, const float *y,
+                                   const float *hidden, const float *alpha, const float *bias,
+                                   const float *coefficients, float *out, int64_t n_rows,
+                                   void *stream);
+
 /* Workspace of o2mi_radial_backward_f32 (non-zero when dalpha or dbias is
  * requested). */
 size_t o2mi_radial_backward_workspace_bytes(const o2mi_radial_plan *plan, int64_t n_rows,
@@ -175,6 +188,39 @@ int o2mi_radial_backward_f32(const o2mi_radial_plan *plan, const float *x, const
                              float *dy, float *dhidden, float *dalpha, float *dbias,
                              void *workspace, size_t workspace_bytes, int64_t n_rows,
                              int needed, void *stream);
+
+/* o2mi_radial_backward_f32 with the gathered first input of
+ * o2mi_radial_forward_gather_f32.  dx_edges ([n_rows, W1]) receives the
+ * adjoint of each edge's gathered row; o2mi_rows_segment_sum_f32 reduces it
+ * onto the table rows.  Workspace as o2mi_radial_backward_workspace_bytes. */
+int o2mi_radial_backward_gather_f32(const o2mi_radial_plan *plan, const float *x_table,
+                                    int64_t table_rows, const int64_t *index, const float *y,
+                                    const float *hidden, const float *alpha, const float *bias,
+                                    const float *coefficients, const float *grad_output,
+                                    float *dx_edges, float *dy, float *dhidden, float *dalpha,
+                                    float *dbias, void *workspace, size_t workspace_bytes,
+                                    int64_t n_rows, int needed, void *stream);
+
+/* ---- row gather and deterministic row segment sums -------------------------
+ * The node <-> edge data movement of a message-passing layer around the
+ * radial product.  No counterpart in the reference, which gathers with
+ * torch indexing and scatters with atomic index_add outside its chain
+ * (docs/RADIAL.md:97-99). */
+
+/* dst[e, :] = src[index[e], :] for e < n_rows ([n_rows, width] f32); an
+ * index outside [0, src_rows) writes a zero row. */
+int o2mi_rows_gather_f32(const float *src, int64_t src_rows, const int64_t *index,
+                         int64_t n_rows, int64_t width, float *dst, void *stream);
+
+/* dst[s, :] = sum of rows[order[k], :] for k in [offsets[s], offsets[s+1]),
+ * added in increasing k (s < n_segments; offsets has n_segments + 1 entries;
+ * runs are clamped to [0, n_rows) and entries of `order` outside [0, n_rows)
+ * are skipped).  With `order` a stable sort of the edges by index and
+ * `offsets` each table row's run, this is the adjoint of o2mi_rows_gather_f32
+ * in a fixed summation order (bitwise reproducible). */
+int o2mi_rows_segment_sum_f32(const float *rows, int64_t n_rows, int64_t width,
+                              const int64_t *order, const int64_t *offsets, int64_t n_segments,
+                              float *dst, void *stream);
 
 /* Kernel timing for measurement harnesses (no counterpart in the reference):
  * while enabled, every forward/backward call records a HIP event pair around

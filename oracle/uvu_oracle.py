@@ -12,7 +12,11 @@ Restates ``uvu_o2.py`` of Parity-LRX/ICTC-O2-HP:
   (``uvu_o2.py:50-73``); weights shared [P*C*V] or per row [N, P*C*V];
 * backward: the exact transpose (dx, dy, dw), written out;
 * radial: ``tp(left, angular, hidden @ alpha^T + bias)`` (``radial_uvu.py:52``) and
-  its chain rule to hidden, alpha, bias.
+  its chain rule to hidden, alpha, bias;
+* gathered radial: ``left = table[index]``, the node -> edge gather a model does
+  before the reference's radial chain (docs/RADIAL.md:97-99), whose adjoint adds
+  each edge's row adjoint onto its table row (``np.add.at``); an index outside
+  the table reads a zero row and receives nothing.
 
 Pinned by tests/golden/uvu_tables.json and uvu_vectors.npz (recorded from the
 reference), finite differences and the bilinear adjoint identity.
@@ -153,3 +157,35 @@ def radial_backward(plan: UvuOraclePlan, x, y, hidden, alpha, bias, grad):
         w = w + np.asarray(bias, np.float64)
     dx, dy, dw = backward(plan, x, y, w, grad, shared=False)
     return dx, dy, dw @ alpha, dw.T @ hidden, (dw.sum(axis=0) if bias is not None else None)
+
+
+def gather(table, index):
+    """table[index] with a zero row for an index outside [0, len(table))."""
+    table = np.asarray(table)
+    index = np.asarray(index, dtype=np.int64)
+    valid = (index >= 0) & (index < table.shape[0])
+    out = np.zeros((index.shape[0], table.shape[1]), dtype=table.dtype)
+    out[valid] = table[index[valid]]
+    return out
+
+
+def scatter_add(rows, index, n):
+    """Adjoint of ``gather``: sum rows[e] into row index[e] of an [n, width] array."""
+    rows = np.asarray(rows)
+    index = np.asarray(index, dtype=np.int64)
+    valid = (index >= 0) & (index < n)
+    out = np.zeros((n, rows.shape[1]), dtype=rows.dtype)
+    np.add.at(out, index[valid], rows[valid])
+    return out
+
+
+def radial_gather_forward(plan: UvuOraclePlan, table, index, y, hidden, alpha, bias):
+    """radial_forward on the gathered rows table[index]."""
+    return radial_forward(plan, gather(table, index), y, hidden, alpha, bias)
+
+
+def radial_gather_backward(plan: UvuOraclePlan, table, index, y, hidden, alpha, bias, grad):
+    """(dtable, dy, dhidden, dalpha, dbias): radial_backward on the gathered
+    rows, with the row adjoints added onto the table."""
+    dx, dy, dh, da, db = radial_backward(plan, gather(table, index), y, hidden, alpha, bias, grad)
+    return scatter_add(dx, index, np.asarray(table).shape[0]), dy, dh, da, db
