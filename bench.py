@@ -49,6 +49,8 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="time budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-stream-ceiling", action="store_true",
+                   help="skip the HBM streaming-ceiling probe (tp workload)")
     p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu", "grid"),
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays")
     p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
@@ -110,6 +112,22 @@ def _sample_stats(samples):
         return None, None
     q = statistics.quantiles(samples, n=4) if len(samples) >= 2 else [samples[0]] * 3
     return statistics.median(samples), q[2] - q[0]
+
+
+def _stream_ceiling(rows, width):
+    """Best GB/s of plain 3-read/2-write and 2-read/1-write row streams on this
+    GPU (ictc_o2_hp/o2mi_stream_probe, a child process), or None."""
+    import subprocess
+    probe = REPO / "ictc-o2-hp_amd" / "ictc_o2_hp" / "o2mi_stream_probe"
+    if not probe.exists():
+        return None
+    width = width if width <= 4096 and width % 2 == 0 else 3328
+    try:
+        proc = subprocess.run([str(probe), str(rows), str(width)], capture_output=True,
+                              text=True, timeout=120)
+        return json.loads(proc.stdout) if proc.returncode == 0 else None
+    except (OSError, ValueError, subprocess.TimeoutExpired):
+        return None
 
 
 def _traffic(path: Path, key: str):
@@ -554,6 +572,13 @@ def tp_main(args):
     }
     del x, y, cot
     torch.cuda.empty_cache()
+    if not args.no_stream_ceiling:
+        ceiling = _stream_ceiling(n, width)
+        if ceiling:
+            record["stream_ceiling"] = ceiling
+            record["roofline"]["frac_of_stream_ceiling"] = achieved / ceiling["read3_write2_GBps"]
+            record["kernels_ms"]["forward_frac_of_stream_ceiling"] = (
+                alg_fwd / (fwd_avg * 1e-3) / 1e9 / ceiling["read2_write1_GBps"])
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = _cpu_baseline(args.channels, args.m_max, args.parity, width,
                                                args.cpu_seconds)
