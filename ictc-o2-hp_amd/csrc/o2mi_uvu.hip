@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256) void uvu_weight_shared_kernel(
 // a single writer per element and need no atomics.  x, y and g of the row are
 // staged in LDS.  Coupling slot order is [out c][in1 a][in2 b].
 constexpr int kRowThreads = 256;
+constexpr int kRowBatch = 4;  // weight loads in flight per thread
 using f4v = float __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float group_sum(float v, int group) {
@@ -298,20 +299,32 @@ __global__ __launch_bounds__(kRowThreads) void uvu_row_forward_kernel(
   for (int p = 0; p < pr.P; ++p) {
     const RowPath rp = row_path(pr, p);
     const f4v* wp = wrow + rp.r.wo / 4;
-    for (int q = threadIdx.x; q < per_path; q += kRowThreads) {
-      const f4v wv = __builtin_nontemporal_load(wp + q);
-      const int u = q / G, v0 = 4 * (q - u * G);
-      float p0, p1;
-      lane_project(wv, sy, rp.r.yo, rp.r.yd, v0, p0, p1);
-      p0 = group_sum(p0, G);
-      p1 = group_sum(p1, G);
-      if (v0 == 0) {
-        const float a0 = sx[rp.r.xo + u * rp.r.xd];
-        const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
-        float* o = so + rp.r.oo + u * rp.r.od;
-        const float* c = rp.c;
-        o[0] += a0 * (c[0] * p0 + c[1] * p1) + a1 * (c[2] * p0 + c[3] * p1);
-        if (rp.r.od == 2) o[1] += a0 * (c[4] * p0 + c[5] * p1) + a1 * (c[6] * p0 + c[7] * p1);
+    // kRowBatch weight loads per thread are issued before any of them is used,
+    // so each wave keeps kRowBatch KiB of the weight stream in flight.
+    for (int q0 = threadIdx.x; q0 < per_path; q0 += kRowBatch * kRowThreads) {
+      f4v wv[kRowBatch];
+#pragma unroll
+      for (int k = 0; k < kRowBatch; ++k) {
+        const int q = q0 + k * kRowThreads;
+        if (q < per_path) wv[k] = __builtin_nontemporal_load(wp + q);
+      }
+#pragma unroll
+      for (int k = 0; k < kRowBatch; ++k) {
+        const int q = q0 + k * kRowThreads;
+        if (q >= per_path) break;
+        const int u = q / G, v0 = 4 * (q - u * G);
+        float p0, p1;
+        lane_project(wv[k], sy, rp.r.yo, rp.r.yd, v0, p0, p1);
+        p0 = group_sum(p0, G);
+        p1 = group_sum(p1, G);
+        if (v0 == 0) {
+          const float a0 = sx[rp.r.xo + u * rp.r.xd];
+          const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
+          float* o = so + rp.r.oo + u * rp.r.od;
+          const float* c = rp.c;
+          o[0] += a0 * (c[0] * p0 + c[1] * p1) + a1 * (c[2] * p0 + c[3] * p1);
+          if (rp.r.od == 2) o[1] += a0 * (c[4] * p0 + c[5] * p1) + a1 * (c[6] * p0 + c[7] * p1);
+        }
       }
     }
   }
@@ -356,46 +369,60 @@ __global__ __launch_bounds__(kRowThreads) void uvu_row_backward_kernel(
     for (int k = begin; k < end; ++k) {
       const RowPath rp = row_path(pr, pr.order2[k]);
       const float* c = rp.c;
-      for (int q = threadIdx.x; q < per_path; q += kRowThreads) {
-        const int u = q / G, v0 = 4 * (q - u * G);
-        const float a0 = sx[rp.r.xo + u * rp.r.xd];
-        const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
-        const float g0 = sg[rp.r.oo + u * rp.r.od];
-        const float g1 = rp.r.od == 2 ? sg[rp.r.oo + u * rp.r.od + 1] : 0.f;
-        // r_b = d out / d proj_b for this (row, path, u).
-        const float r0 = a0 * (c[0] * g0 + c[4] * g1) + a1 * (c[2] * g0 + c[6] * g1);
-        const float r1 = a0 * (c[1] * g0 + c[5] * g1) + a1 * (c[3] * g0 + c[7] * g1);
-        const float* yv = sy + yo + yd * v0;
-        if (want_w) {
-          f4v d;
-          if (yd == 2) {
-            d.x = r0 * yv[0] + r1 * yv[1];
-            d.y = r0 * yv[2] + r1 * yv[3];
-            d.z = r0 * yv[4] + r1 * yv[5];
-            d.w = r0 * yv[6] + r1 * yv[7];
-          } else {
-            d.x = r0 * yv[0];
-            d.y = r0 * yv[1];
-            d.z = r0 * yv[2];
-            d.w = r0 * yv[3];
-          }
-          __builtin_nontemporal_store(d, dwrow + rp.r.wo / 4 + q);
-        }
+      const f4v* wp = wrow + rp.r.wo / 4;
+      for (int q0 = threadIdx.x; q0 < per_path; q0 += kRowBatch * kRowThreads) {
+        f4v wb[kRowBatch];
         if (read_w) {
-          const f4v wv = __builtin_nontemporal_load(wrow + rp.r.wo / 4 + q);
-          dy[0][0] += wv.x * r0; dy[0][1] += wv.x * r1;
-          dy[1][0] += wv.y * r0; dy[1][1] += wv.y * r1;
-          dy[2][0] += wv.z * r0; dy[2][1] += wv.z * r1;
-          dy[3][0] += wv.w * r0; dy[3][1] += wv.w * r1;
-          if (want_x) {
-            float p0, p1;
-            lane_project(wv, sy, yo, yd, v0, p0, p1);
-            p0 = group_sum(p0, G);
-            p1 = group_sum(p1, G);
-            if (v0 == 0) {
-              float* d = sdx + rp.r.xo + u * rp.r.xd;
-              d[0] += g0 * (c[0] * p0 + c[1] * p1) + g1 * (c[4] * p0 + c[5] * p1);
-              if (rp.r.xd == 2) d[1] += g0 * (c[2] * p0 + c[3] * p1) + g1 * (c[6] * p0 + c[7] * p1);
+#pragma unroll
+          for (int b = 0; b < kRowBatch; ++b) {
+            const int q = q0 + b * kRowThreads;
+            if (q < per_path) wb[b] = __builtin_nontemporal_load(wp + q);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kRowBatch; ++b) {
+          const int q = q0 + b * kRowThreads;
+          if (q >= per_path) break;
+          const int u = q / G, v0 = 4 * (q - u * G);
+          const float a0 = sx[rp.r.xo + u * rp.r.xd];
+          const float a1 = rp.r.xd == 2 ? sx[rp.r.xo + u * rp.r.xd + 1] : 0.f;
+          const float g0 = sg[rp.r.oo + u * rp.r.od];
+          const float g1 = rp.r.od == 2 ? sg[rp.r.oo + u * rp.r.od + 1] : 0.f;
+          // r_b = d out / d proj_b for this (row, path, u).
+          const float r0 = a0 * (c[0] * g0 + c[4] * g1) + a1 * (c[2] * g0 + c[6] * g1);
+          const float r1 = a0 * (c[1] * g0 + c[5] * g1) + a1 * (c[3] * g0 + c[7] * g1);
+          const float* yv = sy + yo + yd * v0;
+          if (want_w) {
+            f4v d;
+            if (yd == 2) {
+              d.x = r0 * yv[0] + r1 * yv[1];
+              d.y = r0 * yv[2] + r1 * yv[3];
+              d.z = r0 * yv[4] + r1 * yv[5];
+              d.w = r0 * yv[6] + r1 * yv[7];
+            } else {
+              d.x = r0 * yv[0];
+              d.y = r0 * yv[1];
+              d.z = r0 * yv[2];
+              d.w = r0 * yv[3];
+            }
+            __builtin_nontemporal_store(d, dwrow + rp.r.wo / 4 + q);
+          }
+          if (read_w) {
+            const f4v wv = wb[b];
+            dy[0][0] += wv.x * r0; dy[0][1] += wv.x * r1;
+            dy[1][0] += wv.y * r0; dy[1][1] += wv.y * r1;
+            dy[2][0] += wv.z * r0; dy[2][1] += wv.z * r1;
+            dy[3][0] += wv.w * r0; dy[3][1] += wv.w * r1;
+            if (want_x) {
+              float p0, p1;
+              lane_project(wv, sy, yo, yd, v0, p0, p1);
+              p0 = group_sum(p0, G);
+              p1 = group_sum(p1, G);
+              if (v0 == 0) {
+                float* d = sdx + rp.r.xo + u * rp.r.xd;
+                d[0] += g0 * (c[0] * p0 + c[1] * p1) + g1 * (c[4] * p0 + c[5] * p1);
+                if (rp.r.xd == 2) d[1] += g0 * (c[2] * p0 + c[3] * p1) + g1 * (c[6] * p0 + c[7] * p1);
+              }
             }
           }
         }
