@@ -60,14 +60,23 @@ bool o2mi_timing_begin(hipStream_t s, O2miTimed* launch, int kind) {
   launch->kind = kind;
   launch->start = take_event();
   launch->stop = take_event();
-  if (!launch->start || !launch->stop) return false;
-  return hipEventRecord(launch->start, s) == hipSuccess;
+  if (launch->start && launch->stop && hipEventRecord(launch->start, s) == hipSuccess)
+    return true;
+  // Untimed launch: return whatever events were taken to the pool.
+  if (launch->start) g_event_pool.push_back(launch->start);
+  if (launch->stop) g_event_pool.push_back(launch->stop);
+  return false;
 }
 
 void o2mi_timing_end(hipStream_t s, O2miTimed* launch) {
-  if (hipEventRecord(launch->stop, s) != hipSuccess) return;
+  const bool recorded = hipEventRecord(launch->stop, s) == hipSuccess;
   std::lock_guard<std::mutex> lock(g_timing_mu);
-  g_timed.push_back(*launch);
+  if (recorded) {
+    g_timed.push_back(*launch);
+  } else {
+    g_event_pool.push_back(launch->start);
+    g_event_pool.push_back(launch->stop);
+  }
 }
 
 namespace {

@@ -120,9 +120,12 @@ def o2_backward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
     grad_left = torch.empty_like(left)
     grad_right = torch.empty_like(right)
     grad_weight = torch.empty_like(weight)
-    ws_bytes = native.workspace_bytes(n_rows)
-    workspace = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=left.device)
+    # The workspace size depends on the device's CU count: query it on the
+    # tensors' device, like the launch.
     with torch.cuda.device(left.device):
+        ws_bytes = native.workspace_bytes(n_rows)
+        workspace = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32,
+                                device=left.device)
         native.backward(left.data_ptr(), right.data_ptr(), weight.data_ptr(),
                         grad_output.data_ptr(), grad_left.data_ptr(), grad_right.data_ptr(),
                         grad_weight.data_ptr(), workspace.data_ptr(), ws_bytes, n_rows, 7,

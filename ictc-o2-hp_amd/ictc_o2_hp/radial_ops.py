@@ -138,10 +138,10 @@ def _backward_impl(left, angular, radial, alpha, bias, grad_output, info, coeffi
         left, radial, alpha = _aligned(left), _aligned(radial), _aligned(alpha)
         grad_output = _aligned(grad_output)
         angular = angular.contiguous()
-        ws_bytes = int(lib.o2mi_radial_backward_workspace_bytes(plan, rows, needed))
-        workspace = torch.empty(max(4, (ws_bytes + 3) // 4), dtype=torch.float32,
-                                device=left.device)
-        with torch.cuda.device(left.device):
+        with torch.cuda.device(left.device):  # workspace size and launch on one device
+            ws_bytes = int(lib.o2mi_radial_backward_workspace_bytes(plan, rows, needed))
+            workspace = torch.empty(max(4, (ws_bytes + 3) // 4), dtype=torch.float32,
+                                    device=left.device)
             _native.check(lib.o2mi_radial_backward_f32(
                 plan, left.data_ptr(), angular.data_ptr(), radial.data_ptr(), alpha.data_ptr(),
                 _ptr(bias) if has_bias else None, coefficients.data_ptr(),
@@ -359,10 +359,10 @@ def _gather_backward_impl(table, index, angular, radial, alpha, bias, grad_outpu
             table, radial, alpha = _aligned(table), _aligned(radial), _aligned(alpha)
             grad_output = _aligned(grad_output)
             angular = angular.contiguous()
-            ws_bytes = int(lib.o2mi_radial_backward_workspace_bytes(plan, rows, needed))
-            workspace = torch.empty(max(4, (ws_bytes + 3) // 4), dtype=torch.float32,
-                                    device=table.device)
-            with torch.cuda.device(table.device):
+            with torch.cuda.device(table.device):  # workspace size and launch on one device
+                ws_bytes = int(lib.o2mi_radial_backward_workspace_bytes(plan, rows, needed))
+                workspace = torch.empty(max(4, (ws_bytes + 3) // 4), dtype=torch.float32,
+                                        device=table.device)
                 _native.check(lib.o2mi_radial_backward_gather_f32(
                     plan, table.data_ptr(), table.shape[0], index.data_ptr(), angular.data_ptr(),
                     radial.data_ptr(), alpha.data_ptr(), _ptr(bias) if has_bias else None,
