@@ -230,3 +230,76 @@ def test_native_library_is_loaded():
     import os
     maps = open(f"/proc/{os.getpid()}/maps").read()
     assert _native.LIBRARY_NAME in maps
+
+
+def _normalized_error_t(ref: torch.Tensor, got: torch.Tensor) -> float:
+    """The reference's metric (oracle normalized_error) on device tensors."""
+    scale = max(1e-7, ref.abs().max().item(), got.abs().max().item())
+    return (ref - got.to(ref.dtype)).abs().max().item() / scale
+
+
+def _headline_inputs(seed):
+    module = _module(128, 6, "full", seed=seed)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    n = 131072
+    x = torch.randn(n, module.representation_dimension, device="cuda", generator=gen)
+    y = torch.randn(x.shape, device="cuda", generator=gen)
+    g = torch.randn(x.shape, device="cuda", generator=gen)
+    return module, x, y, g
+
+
+def test_headline_full_size_rows_vs_oracle():
+    """BASELINE headline shape (N=131072, C128 m6 full) at its full launch
+    geometry: 256 random rows against the fp64 oracle, dw from a cotangent
+    that is zero outside those rows (so the oracle's dw over them is exact)."""
+    print("case headline N=131072 C128 m6 full, 256-row oracle subset", flush=True)
+    module, x, y, g = _headline_inputs(131)
+    rows = torch.randperm(x.shape[0], generator=torch.Generator().manual_seed(131))[:256]
+    rows = rows.sort().values.cuda()
+    mask = torch.zeros(x.shape[0], 1, device="cuda")
+    mask[rows] = 1.0
+    g = g * mask
+    xr, yr = x.clone().requires_grad_(), y.clone().requires_grad_()
+    out = module(xr, yr)
+    dx, dy, dw = torch.autograd.grad(out, (xr, yr, module.weight), g)
+    plan = O.OraclePlan(128, 6, "full")
+    w = module.weight.detach().double().cpu().numpy()
+    xs, ys, gs = (t[rows].double().cpu().numpy() for t in (x, y, g))
+    ref_dx, ref_dy, ref_dw = O.backward(plan, xs, ys, w, gs)
+    errors = {
+        "out": O.normalized_error(O.forward(plan, xs, ys, w),
+                                  out.detach()[rows].double().cpu().numpy()),
+        "dx": O.normalized_error(ref_dx, dx[rows].double().cpu().numpy()),
+        "dy": O.normalized_error(ref_dy, dy[rows].double().cpu().numpy()),
+        "dw": O.normalized_error(ref_dw, dw.double().cpu().numpy()),
+    }
+    assert max(errors.values()) <= TOL, errors
+
+
+def test_headline_full_size_every_row_vs_fp64_algebra():
+    """BASELINE headline shape, every row and the full dw: the kernels against
+    the PyTorch algebra (the reference's fast_o2.py map, pinned to the oracle
+    on the CPU) evaluated in float64 on the GPU in row chunks."""
+    from ictc_o2_hp.torch_algebra import flat_forward
+    print("case headline N=131072 C128 m6 full, all rows vs fp64 algebra", flush=True)
+    module, x, y, g = _headline_inputs(132)
+    xr, yr = x.clone().requires_grad_(), y.clone().requires_grad_()
+    out = module(xr, yr)
+    dx, dy, dw = torch.autograd.grad(out, (xr, yr, module.weight), g)
+    plan = module._plan
+    w64 = module.weight.detach().double().requires_grad_()
+    worst = {"out": 0.0, "dx": 0.0, "dy": 0.0}
+    dw64 = torch.zeros_like(w64)
+    for s in range(0, x.shape[0], 16384):
+        e = s + 16384
+        a = x[s:e].double().requires_grad_()
+        b = y[s:e].double().requires_grad_()
+        ref = flat_forward(a, b, w64, plan)
+        ra, rb, rw = torch.autograd.grad(ref, (a, b, w64), g[s:e].double())
+        dw64 += rw
+        for name, r, got in (("out", ref.detach(), out[s:e]), ("dx", ra, dx[s:e]),
+                             ("dy", rb, dy[s:e])):
+            worst[name] = max(worst[name], _normalized_error_t(r, got))
+        del ref, ra, rb, a, b
+    worst["dw"] = _normalized_error_t(dw64, dw)
+    assert max(worst.values()) <= TOL, worst
