@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void uvu_weight_shared_kernel(
 // a single writer per element and need no atomics.  x, y and g of the row are
 // staged in LDS.  Coupling slot order is [out c][in1 a][in2 b].
 constexpr int kRowThreads = 256;
-constexpr int kRowBatch = 4;  // weight loads in flight per thread
+constexpr int kRowBatch = 8;  // weight loads in flight per thread (4: +3% step time)
 using f4v = float __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float group_sum(float v, int group) {
