@@ -15,6 +15,12 @@ the reference gathers outside its chain, docs/RADIAL.md:97-99) equals
 fused kernels read the table rows directly, and the table's gradient sums the
 edge adjoints onto table rows in a fixed order (``graph_ops``), so it is
 bitwise reproducible.  An index outside ``[0, nodes)`` reads a zero row.
+
+``out_index=dst, out_rows=n`` (with or without ``left_index``) returns the
+edge -> node aggregation ``[n, input1_dimension]``: each edge's output summed
+onto row ``dst[e]`` in increasing edge order (``graph_ops.scatter_add_rows``,
+deterministic; its backward gathers the node cotangent).  An index outside
+``[0, n)`` is dropped.
 """
 from __future__ import annotations
 
@@ -49,7 +55,22 @@ class RadialUvuTensorProduct(torch.nn.Module):
             radial_ops.register_structure(tp._kernel_metadata_id, tp.channels, tp.m_max,
                                           tp.parity, tp.m_max_in2, tp.parity_in2)
 
-    def forward(self, left, angular, radial_hidden, *, left_index=None):
+    def forward(self, left, angular, radial_hidden, *, left_index=None, out_index=None,
+                out_rows=None):
+        if (out_index is None) != (out_rows is None):
+            raise ValueError("out_index and out_rows must be given together")
+        if out_index is not None:
+            if out_index.ndim != 1 or out_index.dtype not in (torch.int64, torch.int32):
+                raise ValueError("out_index must be a 1-D int64 or int32 tensor")
+            if int(out_rows) < 0:
+                raise ValueError("out_rows must be non-negative")
+            edges = self.forward(left, angular, radial_hidden, left_index=left_index)
+            if edges.ndim != 2 or out_index.shape[0] != edges.shape[0]:
+                raise ValueError("out_index must have one entry per edge of [edges, dim] inputs")
+            if out_index.device != edges.device:
+                raise ValueError("out_index must be on the inputs' device")
+            from . import graph_ops
+            return graph_ops.scatter_add_rows(edges, out_index, int(out_rows))
         if left_index is not None:
             return self._forward_gathered(left, left_index, angular, radial_hidden)
         tp = self.tp

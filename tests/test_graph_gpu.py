@@ -220,3 +220,40 @@ def test_gathered_double_backward(c, hidden):
     want = second_order(ref_module, lin64, t64, index.cpu(), y64, h64)
     for r, a in zip(want, got):
         assert normalized_error(r.detach().numpy(), a.double().cpu().numpy()) <= TOL
+
+
+def test_message_passing_gather_and_aggregate():
+    """left_index (fused gather) and out_index (deterministic edge -> node sum)
+    together, at the configs[4] structure, against the oracle; reproducible."""
+    from ictc_o2_hp import radial_ops
+    print("message passing C64 m4 H64 nodes=1500 edges=6000", flush=True)
+    tp, linear, module, plan = _build(64, 4, 64, 31)
+    assert radial_ops.fused_plan(tp._kernel_metadata_id, 64) is not None
+    rng = np.random.default_rng(31)
+    nodes, edges = 1500, 6000
+    table = rng.standard_normal((nodes, plan.width1)).astype(np.float32)
+    src = rng.integers(0, nodes, size=edges)
+    dst = rng.integers(0, nodes, size=edges)
+    y = rng.standard_normal((edges, plan.width2)).astype(np.float32)
+    h = rng.standard_normal((edges, 64)).astype(np.float32)
+    g = rng.standard_normal((nodes, plan.width1)).astype(np.float32)
+    tt, yt, ht = (torch.from_numpy(a).cuda().requires_grad_() for a in (table, y, h))
+    st, dt = torch.from_numpy(src).cuda(), torch.from_numpy(dst).cuda()
+    params = (tt, yt, ht, linear.weight, linear.bias)
+
+    def run():
+        out = module(tt, yt, ht, left_index=st, out_index=dt, out_rows=nodes)
+        return (out, *torch.autograd.grad(out, params, torch.from_numpy(g).cuda()))
+
+    first, second = run(), run()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    alpha = linear.weight.detach().double().cpu().numpy()
+    bias = linear.bias.detach().double().cpu().numpy()
+    args = (plan, table.astype(np.float64), src, y.astype(np.float64), h.astype(np.float64),
+            alpha, bias)
+    want = U.scatter_add(U.radial_gather_forward(*args), dst, nodes)
+    assert normalized_error(want, first[0].detach().cpu().numpy()) <= TOL
+    ref = U.radial_gather_backward(*args, U.gather(g.astype(np.float64), dst))
+    for r, a in zip(ref, first[1:]):
+        assert normalized_error(r, a.double().cpu().numpy()) <= TOL
