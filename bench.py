@@ -282,7 +282,10 @@ def radial_main(args):
         "kernels_ms": per, "kernels_TFLOPs": tflops, "wall_ms_per_step": wall_ms,
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": tflops.get(dominant), "peak": peak, "unit": "TFLOP/s",
-                     "frac": (tflops.get(dominant) or 0.0) / peak, "traffic": None},
+                     "frac": (tflops.get(dominant) or 0.0) / peak,
+                     "traffic": _traffic(REPO / "profiles" / "traffic.json",
+                                         f"{dominant}_C64_m4_canonical_E{edges}"
+                                         + ("" if not args.torch_gather else "_torch_gather"))},
     }
     del chain, node_feats, basis, angular, cot
     torch.cuda.empty_cache()
@@ -313,13 +316,15 @@ def uvu_main(args):
     def step():
         return torch.autograd.grad(run(x, y, w), (x, y, w), cot)
 
-    ms_per_step, wall_ms, _, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    ms_per_step, wall_ms, kinds, samples = _timed_steps(torch, step, args.steps, args.warmup)
     median, iqr = _sample_stats(samples)
     w1, w2, pw = module.input1_dimension, module.input2_dimension, module.weight_numel
-    # Algorithmic bytes: forward reads x, y, w, writes out; backward reads x, y,
-    # w, g and writes dx, dy, dw.
-    alg = 4.0 * n * (2 * w1 + w2 + pw + w1) + 4.0 * n * (3 * w1 + w2 + pw + w1 + w2 + pw)
-    achieved = alg / (ms_per_step * 1e-3) / 1e9
+    # Algorithmic bytes per launch: the forward reads x, y, w and writes out;
+    # the backward reads x, g, y, w and writes dx, dy, dw.
+    alg_fwd = 4.0 * n * (2 * w1 + w2 + pw)
+    alg_bwd = 4.0 * n * (3 * w1 + 2 * w2 + 2 * pw)
+    per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in ("uvu_forward", "uvu_backward")}
+    bwd_gbs = alg_bwd / (per["uvu_backward"] * 1e-3) / 1e9 if per["uvu_backward"] else None
     record = {
         "metric": "uvu fwd + VJP rows/s (configs[3] shape, reduced N); step HBM GB/s",
         "value": n / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1,
@@ -330,9 +335,15 @@ def uvu_main(args):
                                "fwd+VJP (x, y, w)", "rows": n, "weights_per_row": pw},
         "ms_per_step_median": median, "ms_per_step_iqr": iqr,
         "wall_ms_per_step": wall_ms,
-        "roofline": {"bound": "hbm", "kernel": "uvu step", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None},
+        "achieved_step_GBps": (alg_fwd + alg_bwd) / (ms_per_step * 1e-3) / 1e9,
+        "kernels_ms": {"forward": per["uvu_forward"], "backward": per["uvu_backward"],
+                       "forward_GBps": alg_fwd / (per["uvu_forward"] * 1e-3) / 1e9
+                       if per["uvu_forward"] else None},
+        "roofline": {"bound": "hbm", "kernel": "uvu_row_backward_kernel", "achieved": bwd_gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": bwd_gbs / HBM_PEAK_GBS if bwd_gbs else None,
+                     "traffic": _traffic(REPO / "profiles" / "traffic.json",
+                                         f"uvu_backward_C128_V32_m4_full_N{n}")},
     }
     print(json.dumps(record), flush=True)
 

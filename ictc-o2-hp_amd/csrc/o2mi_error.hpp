@@ -15,7 +15,9 @@ enum {
   O2MI_TIMED_RADIAL_FORWARD = 2,
   O2MI_TIMED_RADIAL_BACKWARD = 3,
   O2MI_TIMED_RADIAL_WEIGHT = 4,
-  O2MI_TIMED_KINDS = 5,
+  O2MI_TIMED_UVU_FORWARD = 5,   // the per-row-weight uvu kernels
+  O2MI_TIMED_UVU_BACKWARD = 6,
+  O2MI_TIMED_KINDS = 7,
 };
 
 struct O2miTimed {

@@ -534,8 +534,11 @@ int o2mi_uvu_forward_f32(const o2mi_uvu_problem* problem, const float* x, const 
   if (!x || !y || !w || !out) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (const size_t lds = row_kernel_lds(pr, false, w, nullptr)) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
     hipLaunchKernelGGL(uvu_row_forward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
                        pr, x, y, w, out);
+    if (timing) o2mi_timing_end(s, &timed);
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu forward launch failed");
   }
@@ -571,8 +574,11 @@ int o2mi_uvu_backward_f32(const o2mi_uvu_problem* problem, const float* x, const
   if (((needed & 1) && !gx) || ((needed & 2) && !gy) || ((needed & 4) && !gw))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
   if (const size_t lds = row_kernel_lds(pr, true, w, (needed & 4) ? gw : nullptr)) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);
     hipLaunchKernelGGL(uvu_row_backward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
                        pr, x, y, w, g, gx, gy, gw, needed);
+    if (timing) o2mi_timing_end(s, &timed);
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu backward launch failed");
   }

@@ -214,7 +214,8 @@ def kernel_timing_read():
     return f_ms.value, f_n.value, b_ms.value, b_n.value
 
 
-TIMED_KINDS = ("tp_forward", "tp_backward", "radial_forward", "radial_backward", "radial_weight")
+TIMED_KINDS = ("tp_forward", "tp_backward", "radial_forward", "radial_backward", "radial_weight",
+               "uvu_forward", "uvu_backward")
 
 
 def kernel_timing_read_kinds() -> dict:

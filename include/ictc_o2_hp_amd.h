@@ -231,7 +231,8 @@ int o2mi_kernel_timing(int enable);
 int o2mi_kernel_timing_read(double *forward_ms, int *forward_count, double *backward_ms,
                             int *backward_count);
 /* Same, per kind: 0 TP forward, 1 TP backward, 2 radial forward, 3 radial
- * input adjoints (dx, dy, dhidden), 4 radial affine adjoints (dalpha, dbias).
+ * input adjoints (dx, dy, dhidden), 4 radial affine adjoints (dalpha, dbias),
+ * 5 uvu per-row-weight forward, 6 uvu per-row-weight backward.
  * ms[k] and counts[k] for k < n_kinds. */
 int o2mi_kernel_timing_read_kinds(double *ms, int *counts, int n_kinds);
 
