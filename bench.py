@@ -51,8 +51,10 @@ def _args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-stream-ceiling", action="store_true",
                    help="skip the HBM streaming-ceiling probe (tp workload)")
-    p.add_argument("--workload", default="tp", choices=("tp", "radial", "uvu", "grid"),
-                   help="grid: every configs[2] point (and configs[1]) as HIP-graph replays")
+    p.add_argument("--workload", default="tp",
+                   choices=("tp", "radial", "uvu", "grid", "radial-grid"),
+                   help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
+                        "radial-grid: the reference's published radial-chain points")
     p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
     p.add_argument("--copy-probe", action="store_true",
                    help="after the run, copy 512 MiB 3 times with an elementwise kernel "
@@ -489,6 +491,93 @@ def grid_main(args):
         Path(args.grid_out).write_text(json.dumps(records, indent=1))
 
 
+# The reference's published radial chain (docs/RADIAL_PERFORMANCE.md:17-26, :37-52; A100,
+# torch.compile): Linear(16,64)-SiLU-Linear(64,64)-SiLU-Linear(64,P*C,bias=False) -> V=1
+# uvu TP, first/output full parity, angular canonical, m_max 6, per-edge inputs (no gather).
+# (edges, C) -> (forward ms, full VJP ms).
+A100_RADIAL = {
+    (131072, 64): (25.991, 114.167), (16384, 64): (3.660, 13.159),
+    (131072, 256): (102.812, 410.604), (32768, 128): (12.808, 50.896),
+    (32768, 64): (6.212, 27.778), (65536, 64): (13.015, 56.530),
+    (32768, 256): (25.843, 100.963), (131072, 128): (51.236, 208.039),
+}
+
+
+def radial_grid_main(args):
+    """The reference's radial-chain benchmark points: compiled forward and full
+    VJP (x, angular, basis and every network parameter), median of 11 samples
+    after 20 warm-ups, as in docs/RADIAL_PERFORMANCE.md:3-11."""
+    import statistics
+    import torch
+    from ictc_o2_hp import RadialUvuTensorProduct, UvuTensorProduct, _native, radial_ops
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.set_float32_matmul_precision("highest")
+    device = torch.device("cuda:0")
+    _native.library()
+    records = []
+    for (edges, c), (ref_fwd, ref_vjp) in sorted(A100_RADIAL.items(), key=lambda kv: kv[0][::-1]):
+        torch.manual_seed(7)
+        tp = UvuTensorProduct(c, 1, 6, parity="full", parity_in2="canonical",
+                              shared_weights=False)
+        trunk = torch.nn.Sequential(torch.nn.Linear(16, 64), torch.nn.SiLU(),
+                                    torch.nn.Linear(64, 64), torch.nn.SiLU())
+        radial = RadialUvuTensorProduct(tp, torch.nn.Linear(64, tp.weight_numel, bias=False))
+
+        class Chain(torch.nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.trunk, self.radial = trunk, radial
+
+            def forward(self, x, angular, basis):
+                return self.radial(x, angular, self.trunk(basis))
+
+        chain = Chain().to(device)
+        gen = torch.Generator(device=device).manual_seed(edges + c)
+        x = torch.randn(edges, tp.input1_dimension, device=device, generator=gen)
+        angular = torch.randn(edges, tp.input2_dimension, device=device, generator=gen)
+        basis = torch.randn(edges, 16, device=device, generator=gen)
+        for t in (x, angular, basis):
+            t.requires_grad_()
+        cot = torch.randn(edges, tp.input1_dimension, device=device, generator=gen)
+        run = torch.compile(chain, fullgraph=True, dynamic=False)
+        params = [x, angular, basis] + list(chain.parameters())
+
+        def forward():
+            return run(x, angular, basis)
+
+        def full_vjp():
+            return torch.autograd.grad(run(x, angular, basis), params, cot)
+
+        times = {}
+        for name, fn in (("forward", forward), ("full_vjp", full_vjp)):
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+            samples = []
+            for _ in range(11):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                samples.append(e0.elapsed_time(e1))
+            times[name] = statistics.median(samples)
+        rec = {"edges": edges, "channels": c, "paths": tp.weight_numel // c,
+               "fused_kernels": radial_ops.fused_plan(tp._kernel_metadata_id, 64) is not None,
+               "forward_ms": times["forward"], "full_vjp_ms": times["full_vjp"],
+               "a100_forward_ms": ref_fwd, "a100_full_vjp_ms": ref_vjp,
+               "speedup_forward": ref_fwd / times["forward"],
+               "speedup_full_vjp": ref_vjp / times["full_vjp"]}
+        records.append(rec)
+        print(json.dumps(rec), flush=True)
+        del chain, run, x, angular, basis, cot
+        torch.cuda.empty_cache()
+    if args.grid_out:
+        Path(args.grid_out).write_text(json.dumps(records, indent=1))
+
+
 def main():
     args = _args()
     if args.gpus != 1:
@@ -497,6 +586,8 @@ def main():
         raise SystemExit(2)
     if args.workload == "grid":
         return grid_main(args)
+    if args.workload == "radial-grid":
+        return radial_grid_main(args)
     if args.workload != "tp":
         (radial_main if args.workload == "radial" else uvu_main)(args)
         return _copy_probe(args)

@@ -28,8 +28,11 @@ import torch.nn.functional as F
 from . import _native, uvu_ops
 
 NAMESPACE = uvu_ops.NAMESPACE
-# Row blocks of the composed path: at most this many generated weight floats.
-_BLOCK_WEIGHT_FLOATS = 1 << 24
+# Row blocks of the composed path: at most this many generated weight floats
+# (2 GiB; the block's weight adjoint takes as much again) and rows.  Small
+# blocks starve the GEMMs and multiply launches: at C = 256 with 254 paths a
+# 64 MiB budget gave 258-row blocks and a 36% slower full VJP.
+_BLOCK_WEIGHT_FLOATS = 1 << 29
 _MAX_BLOCK_ROWS = 16384
 
 _STRUCTURES: dict = {}
