@@ -56,6 +56,8 @@ def _args():
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
                         "radial-grid: the reference's published radial-chain points")
     p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
+    p.add_argument("--grid-set", default="configs2", choices=("configs2", "all"),
+                   help="grid: BASELINE.json configs[2] (96 points) or every published point (240)")
     p.add_argument("--copy-probe", action="store_true",
                    help="after the run, copy 512 MiB 3 times with an elementwise kernel "
                         "(reference traffic for HBM counter calibration)")
@@ -351,42 +353,91 @@ def uvu_main(args):
 
 
 # Published A100 times (ms) of the reference's TensorProduct, forward and
-# forward + full VJP, for every configs[2] point
-# (benchmarks/eqx/results/complete_matrix.csv): "N C m_max parity fwd fwd+VJP".
+# forward + full VJP, for every point of its benchmark matrix
+# (benchmarks/eqx/results/complete_matrix.csv, candidate_ms, 4 significant
+# digits): "N C m_max parity fwd fwd+VJP".  configs[2] is the subset
+# C in {32, 64, 128, 256}, m_max in {1, 4, 6}.
 A100_GRID = (
-    "16384 32 1 c 0.0584 0.302; 16384 32 1 f 0.0809 0.442; 16384 32 4 c 0.2002 0.903;"
-    "16384 32 4 f 0.2074 1.376; 16384 32 6 c 0.3594 1.688; 16384 32 6 f 0.2816 2.399;"
-    "16384 64 1 c 0.0742 0.349; 16384 64 1 f 0.1188 0.636; 16384 64 4 c 0.1889 1.378;"
-    "16384 64 4 f 0.3471 2.500; 16384 64 6 c 0.2586 2.533; 16384 64 6 f 0.4864 4.596;"
-    "16384 128 1 c 0.0998 0.465; 16384 128 1 f 0.1966 1.030; 16384 128 4 c 0.3267 2.537;"
-    "16384 128 4 f 0.6528 4.884; 16384 128 6 c 0.4552 4.674; 16384 128 6 f 0.9083 7.824;"
-    "16384 256 1 c 0.1587 0.689; 16384 256 1 f 0.3564 1.977; 16384 256 4 c 0.6001 4.964;"
-    "16384 256 4 f 1.2252 9.202; 16384 256 6 c 0.8663 9.286; 16384 256 6 f 1.7613 15.263;"
-    "32768 32 1 c 0.0753 0.378; 32768 32 1 f 0.1188 0.647; 32768 32 4 c 0.3569 1.670;"
-    "32768 32 4 f 0.3523 2.500; 32768 32 6 c 0.6666 3.237; 32768 32 6 f 0.4931 4.575;"
-    "32768 64 1 c 0.1004 0.468; 32768 64 1 f 0.1961 1.029; 32768 64 4 c 0.3256 2.549;"
-    "32768 64 4 f 0.6385 4.836; 32768 64 6 c 0.4552 4.909; 32768 64 6 f 0.8980 8.370;"
-    "32768 128 1 c 0.1541 0.683; 32768 128 1 f 0.3512 1.973; 32768 128 4 c 0.5980 4.947;"
-    "32768 128 4 f 1.2518 9.512; 32768 128 6 c 0.8530 8.595; 32768 128 6 f 1.7444 15.108;"
-    "32768 256 1 c 0.2668 1.231; 32768 256 1 f 0.6651 3.859; 32768 256 4 c 1.1484 9.051;"
-    "32768 256 4 f 2.3864 16.630; 32768 256 6 c 1.6707 17.104; 32768 256 6 f 3.4540 30.358;"
-    "65536 32 1 c 0.1019 0.514; 65536 32 1 f 0.1997 1.059; 65536 32 4 c 0.6666 3.218;"
-    "65536 32 4 f 0.6451 4.840; 65536 32 6 c 1.2841 6.345; 65536 32 6 f 0.9062 7.769;"
-    "65536 64 1 c 0.1536 0.686; 65536 64 1 f 0.3507 1.964; 65536 64 4 c 0.5990 4.970;"
-    "65536 64 4 f 1.2145 8.309; 65536 64 6 c 0.8571 8.773; 65536 64 6 f 1.7280 14.956;"
-    "65536 128 1 c 0.2627 1.217; 65536 128 1 f 0.6661 3.844; 65536 128 4 c 1.1459 9.765;"
-    "65536 128 4 f 2.4433 16.648; 65536 128 6 c 1.6451 17.098; 65536 128 6 f 3.4186 30.087;"
-    "65536 256 1 c 0.4844 2.359; 65536 256 1 f 1.2861 7.639; 65536 256 4 c 2.2477 17.669;"
-    "65536 256 4 f 4.7145 33.167; 65536 256 6 c 3.2748 34.414; 65536 256 6 f 6.8444 60.811;"
-    "131072 32 1 c 0.1536 0.781; 131072 32 1 f 0.3533 1.988; 131072 32 4 c 1.2800 6.234;"
-    "131072 32 4 f 1.2298 9.547; 131072 32 6 c 2.5185 11.820; 131072 32 6 f 1.7418 15.075;"
-    "131072 64 1 c 0.2642 1.216; 131072 64 1 f 0.6656 3.829; 131072 64 4 c 1.1469 9.641;"
-    "131072 64 4 f 2.3700 16.430; 131072 64 6 c 1.6476 17.166; 131072 64 6 f 3.3756 30.119;"
-    "131072 128 1 c 0.4782 2.322; 131072 128 1 f 1.2969 7.608; 131072 128 4 c 2.2441 17.495;"
-    "131072 128 4 f 4.7995 33.178; 131072 128 6 c 3.2384 34.168; 131072 128 6 f 6.7779 60.348;"
-    "131072 256 1 c 0.9185 4.545; 131072 256 1 f 2.5313 13.859; 131072 256 4 c 4.4544 35.296;"
-    "131072 256 4 f 9.3507 66.198; 131072 256 6 c 6.4794 68.713;"
-    "131072 256 6 f 13.5434 124.088;"
+    "16384 32 1 c 0.05837 0.3021; 16384 32 1 f 0.0809 0.4424; 16384 32 2 c 0.07782 0.4035;"
+    "16384 32 2 f 0.1106 0.6948; 16384 32 3 c 0.09677 0.556; 16384 32 3 f 0.1669 0.9969;"
+    "16384 32 4 c 0.2002 0.9032; 16384 32 4 f 0.2074 1.376; 16384 32 5 c 0.2724 1.248;"
+    "16384 32 5 f 0.2381 1.857; 16384 32 6 c 0.3594 1.688; 16384 32 6 f 0.2816 2.399;"
+    "16384 64 1 c 0.07424 0.3492; 16384 64 1 f 0.1188 0.6359; 16384 64 2 c 0.1024 0.5207;"
+    "16384 64 2 f 0.1782 1.125; 16384 64 3 c 0.1393 0.7578; 16384 64 3 f 0.2775 1.718;"
+    "16384 64 4 c 0.1889 1.378; 16384 64 4 f 0.3471 2.5; 16384 64 5 c 0.2222 1.892;"
+    "16384 64 5 f 0.4116 3.539; 16384 64 6 c 0.2586 2.533; 16384 64 6 f 0.4864 4.596;"
+    "16384 96 1 c 0.09114 0.4229; 16384 96 1 f 0.1618 0.8479; 16384 96 2 c 0.1311 0.6861;"
+    "16384 96 2 f 0.2596 1.597; 16384 96 3 c 0.1772 1.036; 16384 96 3 f 0.3973 2.583;"
+    "16384 96 4 c 0.2591 2.028; 16384 96 4 f 0.4966 3.702; 16384 96 5 c 0.3082 2.896;"
+    "16384 96 5 f 0.5934 5.299; 16384 96 6 c 0.3594 3.901; 16384 96 6 f 0.706 5.953;"
+    "16384 128 1 c 0.09984 0.4654; 16384 128 1 f 0.1966 1.03; 16384 128 2 c 0.1536 0.7839;"
+    "16384 128 2 f 0.322 2.085; 16384 128 3 c 0.2186 1.228; 16384 128 3 f 0.4818 3.319;"
+    "16384 128 4 c 0.3267 2.537; 16384 128 4 f 0.6528 4.884; 16384 128 5 c 0.3901 3.63;"
+    "16384 128 5 f 0.7726 6.97; 16384 128 6 c 0.4552 4.674; 16384 128 6 f 0.9083 7.824;"
+    "16384 256 1 c 0.1587 0.6886; 16384 256 1 f 0.3564 1.977; 16384 256 2 c 0.255 1.401;"
+    "16384 256 2 f 0.5811 4.064; 16384 256 3 c 0.3732 2.338; 16384 256 3 f 0.9272 6.568;"
+    "16384 256 4 c 0.6001 4.964; 16384 256 4 f 1.225 9.202; 16384 256 5 c 0.7322 6.709;"
+    "16384 256 5 f 1.488 11.87; 16384 256 6 c 0.8663 9.286; 16384 256 6 f 1.761 15.26;"
+    "32768 32 1 c 0.07526 0.3784; 32768 32 1 f 0.1188 0.6472; 32768 32 2 c 0.1034 0.5765;"
+    "32768 32 2 f 0.1782 1.12; 32768 32 3 c 0.1393 0.8351; 32768 32 3 f 0.2755 1.727;"
+    "32768 32 4 c 0.3569 1.67; 32768 32 4 f 0.3523 2.5; 32768 32 5 c 0.4992 2.382;"
+    "32768 32 5 f 0.4137 3.563; 32768 32 6 c 0.6666 3.237; 32768 32 6 f 0.4931 4.575;"
+    "32768 64 1 c 0.1004 0.4685; 32768 64 1 f 0.1961 1.029; 32768 64 2 c 0.1541 0.7895;"
+    "32768 64 2 f 0.3052 2.087; 32768 64 3 c 0.2166 1.235; 32768 64 3 f 0.4951 3.309;"
+    "32768 64 4 c 0.3256 2.549; 32768 64 4 f 0.6385 4.836; 32768 64 5 c 0.3901 3.665;"
+    "32768 64 5 f 0.7644 6.647; 32768 64 6 c 0.4552 4.909; 32768 64 6 f 0.898 8.37;"
+    "32768 96 1 c 0.13 0.6093; 32768 96 1 f 0.279 1.529; 32768 96 2 c 0.2094 1.133;"
+    "32768 96 2 f 0.469 3.092; 32768 96 3 c 0.299 1.898; 32768 96 3 f 0.7219 4.756;"
+    "32768 96 4 c 0.4639 3.931; 32768 96 4 f 0.9324 6.53; 32768 96 5 c 0.5632 5.186;"
+    "32768 96 5 f 1.121 8.926; 32768 96 6 c 0.6646 7.652; 32768 96 6 f 1.331 11.48;"
+    "32768 128 1 c 0.1541 0.683; 32768 128 1 f 0.3512 1.973; 32768 128 2 c 0.256 1.386;"
+    "32768 128 2 f 0.5775 3.96; 32768 128 3 c 0.3763 2.328; 32768 128 3 f 0.9078 5.755;"
+    "32768 128 4 c 0.598 4.947; 32768 128 4 f 1.252 9.512; 32768 128 5 c 0.725 6.499;"
+    "32768 128 5 f 1.477 11.8; 32768 128 6 c 0.853 8.595; 32768 128 6 f 1.744 15.11;"
+    "32768 256 1 c 0.2668 1.231; 32768 256 1 f 0.6651 3.859; 32768 256 2 c 0.4526 2.654;"
+    "32768 256 2 f 1.132 7.51; 32768 256 3 c 0.6953 4.549; 32768 256 3 f 1.814 11.41;"
+    "32768 256 4 c 1.148 9.051; 32768 256 4 f 2.386 16.63; 32768 256 5 c 1.406 12.68;"
+    "32768 256 5 f 2.923 23.5; 32768 256 6 c 1.671 17.1; 32768 256 6 f 3.454 30.36;"
+    "65536 32 1 c 0.1019 0.514; 65536 32 1 f 0.1997 1.059; 65536 32 2 c 0.1567 0.8945;"
+    "65536 32 2 f 0.3036 2.066; 65536 32 3 c 0.2166 1.416; 65536 32 3 f 0.4946 3.326;"
+    "65536 32 4 c 0.6666 3.218; 65536 32 4 f 0.6451 4.84; 65536 32 5 c 0.9492 4.652;"
+    "65536 32 5 f 0.766 6.524; 65536 32 6 c 1.284 6.345; 65536 32 6 f 0.9062 7.769;"
+    "65536 64 1 c 0.1536 0.6856; 65536 64 1 f 0.3507 1.964; 65536 64 2 c 0.2575 1.388;"
+    "65536 64 2 f 0.5652 3.877; 65536 64 3 c 0.3768 2.332; 65536 64 3 f 0.9277 6.338;"
+    "65536 64 4 c 0.599 4.97; 65536 64 4 f 1.214 8.309; 65536 64 5 c 0.7255 7.138;"
+    "65536 64 5 f 1.464 11.82; 65536 64 6 c 0.8571 8.773; 65536 64 6 f 1.728 14.96;"
+    "65536 96 1 c 0.212 0.9928; 65536 96 1 f 0.5202 2.959; 65536 96 2 c 0.3635 2.141;"
+    "65536 96 2 f 0.8837 6.052; 65536 96 3 c 0.5381 3.656; 65536 96 3 f 1.403 8.78;"
+    "65536 96 4 c 0.8817 7.183; 65536 96 4 f 1.802 12.58; 65536 96 5 c 1.07 10.02;"
+    "65536 96 5 f 2.178 17.73; 65536 96 6 c 1.265 13.56; 65536 96 6 f 2.588 22.79;"
+    "65536 128 1 c 0.2627 1.217; 65536 128 1 f 0.6661 3.844; 65536 128 2 c 0.4598 2.649;"
+    "65536 128 2 f 1.115 7.506; 65536 128 3 c 0.6932 4.514; 65536 128 3 f 1.748 11.21;"
+    "65536 128 4 c 1.146 9.765; 65536 128 4 f 2.443 16.65; 65536 128 5 c 1.395 12.68;"
+    "65536 128 5 f 2.883 23.26; 65536 128 6 c 1.645 17.1; 65536 128 6 f 3.419 30.09;"
+    "65536 256 1 c 0.4844 2.359; 65536 256 1 f 1.286 7.639; 65536 256 2 c 0.8407 5.17;"
+    "65536 256 2 f 2.166 14.24; 65536 256 3 c 1.316 7.719; 65536 256 3 f 3.561 22.47;"
+    "65536 256 4 c 2.248 17.67; 65536 256 4 f 4.714 33.17; 65536 256 5 c 2.755 25.17;"
+    "65536 256 5 f 5.762 47.22; 65536 256 6 c 3.275 34.41; 65536 256 6 f 6.844 60.81;"
+    "131072 32 1 c 0.1536 0.7808; 131072 32 1 f 0.3533 1.988; 131072 32 2 c 0.2601 1.617;"
+    "131072 32 2 f 0.5663 4.032; 131072 32 3 c 0.3773 2.714; 131072 32 3 f 0.917 6.525;"
+    "131072 32 4 c 1.28 6.234; 131072 32 4 f 1.23 9.547; 131072 32 5 c 1.845 9.143;"
+    "131072 32 5 f 1.47 11.66; 131072 32 6 c 2.519 11.82; 131072 32 6 f 1.742 15.08;"
+    "131072 64 1 c 0.2642 1.216; 131072 64 1 f 0.6656 3.829; 131072 64 2 c 0.4608 2.647;"
+    "131072 64 2 f 1.083 7.902; 131072 64 3 c 0.6881 4.505; 131072 64 3 f 1.794 11.13;"
+    "131072 64 4 c 1.147 9.641; 131072 64 4 f 2.37 16.43; 131072 64 5 c 1.396 12.78;"
+    "131072 64 5 f 2.862 23.24; 131072 64 6 c 1.648 17.17; 131072 64 6 f 3.376 30.12;"
+    "131072 96 1 c 0.3758 1.88; 131072 96 1 f 1.006 5.414; 131072 96 2 c 0.6641 4.163;"
+    "131072 96 2 f 1.732 10.72; 131072 96 3 c 1.021 6.283; 131072 96 3 f 2.746 17.13;"
+    "131072 96 4 c 1.705 13.77; 131072 96 4 f 3.547 24.69; 131072 96 5 c 2.093 19.97;"
+    "131072 96 5 f 4.283 35.23; 131072 96 6 c 2.474 26.81; 131072 96 6 f 5.101 45.51;"
+    "131072 128 1 c 0.4782 2.322; 131072 128 1 f 1.297 7.608; 131072 128 2 c 0.8607 5.134;"
+    "131072 128 2 f 2.16 14.34; 131072 128 3 c 1.329 7.715; 131072 128 3 f 3.423 22.19;"
+    "131072 128 4 c 2.244 17.49; 131072 128 4 f 4.799 33.18; 131072 128 5 c 2.742 25.24;"
+    "131072 128 5 f 5.7 46.73; 131072 128 6 c 3.238 34.17; 131072 128 6 f 6.778 60.35;"
+    "131072 256 1 c 0.9185 4.545; 131072 256 1 f 2.531 13.86; 131072 256 2 c 1.614 9.164;"
+    "131072 256 2 f 4.236 28.46; 131072 256 3 c 2.579 15.32; 131072 256 3 f 6.652 45.07;"
+    "131072 256 4 c 4.454 35.3; 131072 256 4 f 9.351 66.2; 131072 256 5 c 5.465 50.43;"
+    "131072 256 5 f 11.42 95.81; 131072 256 6 c 6.479 68.71; 131072 256 6 f 13.54 124.1;"
 )
 
 
@@ -447,6 +498,8 @@ def grid_main(args):
     device = torch.device("cuda:0")
     _native.library()
     a100 = _a100_grid()
+    if args.grid_set == "configs2":
+        a100 = {k: v for k, v in a100.items() if k[1] in (32, 64, 128, 256) and k[2] in (1, 4, 6)}
     points = sorted(a100) + [(6400, 128, 6, "full")]
     records = []
     for n, c, m, parity in points:
