@@ -56,6 +56,8 @@ def _args():
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
                         "radial-grid: the reference's published radial-chain points")
     p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
+    p.add_argument("--radial-point", default=None,
+                   help="radial-grid: only this 'edges,channels' point (e.g. 131072,64)")
     p.add_argument("--grid-set", default="configs2", choices=("configs2", "all"),
                    help="grid: BASELINE.json configs[2] (96 points) or every published point (240)")
     p.add_argument("--copy-probe", action="store_true",
@@ -569,7 +571,11 @@ def radial_grid_main(args):
     device = torch.device("cuda:0")
     _native.library()
     records = []
-    for (edges, c), (ref_fwd, ref_vjp) in sorted(A100_RADIAL.items(), key=lambda kv: kv[0][::-1]):
+    points = sorted(A100_RADIAL.items(), key=lambda kv: kv[0][::-1])
+    if args.radial_point:
+        want = tuple(int(v) for v in args.radial_point.split(","))
+        points = [kv for kv in points if kv[0] == want]
+    for (edges, c), (ref_fwd, ref_vjp) in points:
         torch.manual_seed(7)
         tp = UvuTensorProduct(c, 1, 6, parity="full", parity_in2="canonical",
                               shared_weights=False)
@@ -688,6 +694,7 @@ def tp_main(args):
     median, iqr = _sample_stats(samples)
     (fwd_ms, fwd_n), (bwd_ms, bwd_n) = kinds["tp_forward"], kinds["tp_backward"]
 
+    peak_mib = torch.cuda.max_memory_allocated() / 2**20
     alg_step = 4.0 * (8.0 * n * width + 3.0 * pw)
     alg_bwd = 4.0 * (5.0 * n * width + 2.0 * pw)
     alg_fwd = 4.0 * (3.0 * n * width + pw)
@@ -720,6 +727,7 @@ def tp_main(args):
                        "forward_GBps": alg_fwd / (fwd_avg * 1e-3) / 1e9,
                        "launches": [fwd_n, bwd_n]},
         "wall_ms_per_step": wall_ms / args.steps,
+        "peak_allocated_MiB": peak_mib,
         "roofline": {"bound": "hbm", "kernel": "tp_backward_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": _traffic(REPO / "profiles" / "traffic.json",

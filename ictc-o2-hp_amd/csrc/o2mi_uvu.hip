@@ -201,6 +201,176 @@ __global__ __launch_bounds__(256) void uvu_backward_y_kernel(Problem pr,
   }
 }
 
+// ---- Per-row weights with V = 1 (the radial product's composed path) --------
+// Same mapping as the generic kernels (thread = (row, u), so a wave covers
+// consecutive channels of one row and each path's weights are one coalesced
+// load), but paths are taken kV1Batch at a time: their records, weights and
+// x / g / y operands are all loaded before any is used, so a wave has
+// kV1Batch independent loads in flight instead of one.  Each output element
+// still sums its paths in table order (deterministic, as above).
+constexpr int kV1Batch = 8;
+
+__global__ __launch_bounds__(256) void uvu_v1_forward_kernel(Problem pr,
+                                                             const float* __restrict__ x,
+                                                             const float* __restrict__ y,
+                                                             const float* __restrict__ w,
+                                                             float* __restrict__ out) {
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item >= pr.n * pr.C) return;  // no barriers below
+  const int64_t n = item / pr.C;
+  const int u = (int)(item - n * pr.C);
+  const float* xr = x + n * pr.W1;
+  const float* yr = y + n * pr.W2;
+  const float* wr = w + n * pr.wnum + u;
+  float* orow = out + n * pr.W1;
+  for (int k = 0; k < pr.NO; ++k) {
+    int oo, od, begin, end;
+    entry_rec(pr, 0, k, oo, od, begin, end);
+    float acc0 = 0.f, acc1 = 0.f;
+    for (int p0 = begin; p0 < end; p0 += kV1Batch) {
+      float wv[kV1Batch], a0[kV1Batch], a1[kV1Batch], y0[kV1Batch], y1[kV1Batch];
+#pragma unroll
+      for (int b = 0; b < kV1Batch; ++b) {
+        if (p0 + b < end) {
+          const PathRec r = path_rec(pr, p0 + b);
+          wv[b] = wr[r.wo];
+          a0[b] = xr[r.xo + u * r.xd];
+          a1[b] = r.xd == 2 ? xr[r.xo + u * r.xd + 1] : 0.f;
+          y0[b] = yr[r.yo];
+          y1[b] = r.yd == 2 ? yr[r.yo + 1] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kV1Batch; ++b) {
+        if (p0 + b < end) {
+          const float* c = pr.coef + 8 * (p0 + b);
+          const float p0v = wv[b] * y0[b], p1v = wv[b] * y1[b];
+          acc0 += a0[b] * (c[0] * p0v + c[1] * p1v) + a1[b] * (c[2] * p0v + c[3] * p1v);
+          acc1 += a0[b] * (c[4] * p0v + c[5] * p1v) + a1[b] * (c[6] * p0v + c[7] * p1v);
+        }
+      }
+    }
+    orow[oo + u * od] = acc0;
+    if (od == 2) orow[oo + u * od + 1] = acc1;
+  }
+}
+
+// dx (bit 1) and dw (bit 4) for V = 1, paths grouped by first entry.
+__global__ __launch_bounds__(256) void uvu_v1_backward_x_kernel(
+    Problem pr, const float* __restrict__ x, const float* __restrict__ y,
+    const float* __restrict__ w, const float* __restrict__ g, float* __restrict__ gx,
+    float* __restrict__ gw, int needed) {
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item >= pr.n * pr.C) return;
+  const int64_t n = item / pr.C;
+  const int u = (int)(item - n * pr.C);
+  const float* xr = x + n * pr.W1;
+  const float* yr = y + n * pr.W2;
+  const float* gr = g + n * pr.W1;
+  const float* wr = w + n * pr.wnum + u;
+  float* dwr = gw + n * pr.wnum + u;
+  const bool want_x = needed & 1;
+  const bool want_w = (needed & 4) != 0;
+  for (int i = 0; i < pr.NX; ++i) {
+    int xo, xd, begin, end;
+    entry_rec(pr, 1, i, xo, xd, begin, end);
+    const float a0 = xr[xo + u * xd];
+    const float a1 = xd == 2 ? xr[xo + u * xd + 1] : 0.f;
+    float d0 = 0.f, d1 = 0.f;
+    for (int q0 = begin; q0 < end; q0 += kV1Batch) {
+      int pb[kV1Batch], wo[kV1Batch];
+      float wv[kV1Batch], g0[kV1Batch], g1[kV1Batch], y0[kV1Batch], y1[kV1Batch];
+#pragma unroll
+      for (int b = 0; b < kV1Batch; ++b) {
+        if (q0 + b < end) {
+          pb[b] = pr.order1[q0 + b];
+          const PathRec r = path_rec(pr, pb[b]);
+          wo[b] = r.wo;
+          wv[b] = want_x ? wr[r.wo] : 0.f;
+          g0[b] = gr[r.oo + u * r.od];
+          g1[b] = r.od == 2 ? gr[r.oo + u * r.od + 1] : 0.f;
+          y0[b] = yr[r.yo];
+          y1[b] = r.yd == 2 ? yr[r.yo + 1] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kV1Batch; ++b) {
+        if (q0 + b < end) {
+          const float* c = pr.coef + 8 * pb[b];
+          if (want_x) {
+            const float p0v = wv[b] * y0[b], p1v = wv[b] * y1[b];
+            d0 += g0[b] * (c[0] * p0v + c[1] * p1v) + g1[b] * (c[4] * p0v + c[5] * p1v);
+            d1 += g0[b] * (c[2] * p0v + c[3] * p1v) + g1[b] * (c[6] * p0v + c[7] * p1v);
+          }
+          if (want_w) {
+            const float r0 = a0 * (c[0] * g0[b] + c[4] * g1[b]) + a1 * (c[2] * g0[b] + c[6] * g1[b]);
+            const float r1 = a0 * (c[1] * g0[b] + c[5] * g1[b]) + a1 * (c[3] * g0[b] + c[7] * g1[b]);
+            __builtin_nontemporal_store(r0 * y0[b] + r1 * y1[b], dwr + wo[b]);
+          }
+        }
+      }
+    }
+    if (want_x) {
+      gx[n * pr.W1 + xo + u * xd] = d0;
+      if (xd == 2) gx[n * pr.W1 + xo + u * xd + 1] = d1;
+    }
+  }
+}
+
+// dy (bit 2) for V = 1: one wave per row, lanes over u; paths grouped by
+// second entry, kV1Batch at a time; lane partials summed by shuffles.
+__global__ __launch_bounds__(256) void uvu_v1_backward_y_kernel(Problem pr,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ g,
+                                                                float* __restrict__ gy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= pr.n) return;  // whole waves leave together; no barriers below
+  const float* xr = x + n * pr.W1;
+  const float* gr = g + n * pr.W1;
+  const float* wr = w + n * pr.wnum;
+  for (int j = 0; j < pr.NY; ++j) {
+    int yo, yd, begin, end;
+    entry_rec(pr, 2, j, yo, yd, begin, end);
+    float s0 = 0.f, s1 = 0.f;
+    for (int u = lane; u < pr.C; u += 64) {
+      for (int q0 = begin; q0 < end; q0 += kV1Batch) {
+        int pb[kV1Batch];
+        float wv[kV1Batch], a0[kV1Batch], a1[kV1Batch], g0[kV1Batch], g1[kV1Batch];
+#pragma unroll
+        for (int b = 0; b < kV1Batch; ++b) {
+          if (q0 + b < end) {
+            pb[b] = pr.order2[q0 + b];
+            const PathRec r = path_rec(pr, pb[b]);
+            wv[b] = wr[r.wo + u];
+            a0[b] = xr[r.xo + u * r.xd];
+            a1[b] = r.xd == 2 ? xr[r.xo + u * r.xd + 1] : 0.f;
+            g0[b] = gr[r.oo + u * r.od];
+            g1[b] = r.od == 2 ? gr[r.oo + u * r.od + 1] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kV1Batch; ++b) {
+          if (q0 + b < end) {
+            const float* c = pr.coef + 8 * pb[b];
+            const float r0 = a0[b] * (c[0] * g0[b] + c[4] * g1[b]) + a1[b] * (c[2] * g0[b] + c[6] * g1[b]);
+            const float r1 = a0[b] * (c[1] * g0[b] + c[5] * g1[b]) + a1[b] * (c[3] * g0[b] + c[7] * g1[b]);
+            s0 = fmaf(wv[b], r0, s0);
+            s1 = fmaf(wv[b], r1, s1);
+          }
+        }
+      }
+    }
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    if (lane == 0) {
+      gy[n * pr.W2 + yo] = s0;
+      if (yd == 2) gy[n * pr.W2 + yo + 1] = s1;
+    }
+  }
+}
+
 // Shared-weight dw partials: block (chunk of u*V, path p, split s) sums rows
 // of split s; a fixed-order column sum over the splits follows.
 __global__ __launch_bounds__(256) void uvu_weight_shared_kernel(
@@ -542,8 +712,12 @@ int o2mi_uvu_forward_f32(const o2mi_uvu_problem* problem, const float* x, const 
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu forward launch failed");
   }
-  hipLaunchKernelGGL(uvu_forward_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr, x,
-                     y, w, out);
+  if (pr.V == 1 && !pr.shared)
+    hipLaunchKernelGGL(uvu_v1_forward_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr,
+                       x, y, w, out);
+  else
+    hipLaunchKernelGGL(uvu_forward_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr, x,
+                       y, w, out);
   return hipGetLastError() == hipSuccess ? O2MI_OK
                                          : fail(O2MI_ERR_HIP, "uvu forward launch failed");
 }
@@ -582,13 +756,22 @@ int o2mi_uvu_backward_f32(const o2mi_uvu_problem* problem, const float* x, const
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu backward launch failed");
   }
+  const bool v1 = pr.V == 1 && !pr.shared;
   if ((needed & 1) || ((needed & 4) && !pr.shared)) {
-    hipLaunchKernelGGL(uvu_backward_x_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s, pr,
-                       x, y, w, g, gx, gw, needed);
+    if (v1)
+      hipLaunchKernelGGL(uvu_v1_backward_x_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s,
+                         pr, x, y, w, g, gx, gw, needed);
+    else
+      hipLaunchKernelGGL(uvu_backward_x_kernel, dim3(blocks_for(pr.n * pr.C)), dim3(256), 0, s,
+                         pr, x, y, w, g, gx, gw, needed);
   }
   if (needed & 2) {
-    hipLaunchKernelGGL(uvu_backward_y_kernel, dim3((unsigned)((pr.n + 3) / 4)), dim3(256), 0, s,
-                       pr, x, w, g, gy);
+    if (v1)
+      hipLaunchKernelGGL(uvu_v1_backward_y_kernel, dim3((unsigned)((pr.n + 3) / 4)), dim3(256), 0,
+                         s, pr, x, w, g, gy);
+    else
+      hipLaunchKernelGGL(uvu_backward_y_kernel, dim3((unsigned)((pr.n + 3) / 4)), dim3(256), 0, s,
+                         pr, x, w, g, gy);
   }
   if ((needed & 4) && pr.shared && pr.P > 0) {
     const int64_t splits = shared_splits(pr);
