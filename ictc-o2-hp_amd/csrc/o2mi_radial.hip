@@ -65,14 +65,16 @@ int device_cus() {
   return c;
 }
 
-// Edge slices of the affine-adjoint kernel: about one block per CU, whole
-// staged tiles per slice, no empty slice.
+// Edge slices of the affine-adjoint kernel: about one block (slice x channel
+// tile x path group) per CU, whole staged tiles per slice, no empty slice.
 void slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
-  const int64_t tiles_c = p->C / 16;
-  const int64_t want = std::max<int64_t>(1, (device_cus() + tiles_c - 1) / tiles_c);
-  const int64_t edge_tiles = std::max<int64_t>(1, (n + kWeightEdges - 1) / kWeightEdges);
+  const int64_t blocks_per_slice = (int64_t)(p->C / 16) * p->set->weight_groups;
+  const int64_t want =
+      std::max<int64_t>(1, (device_cus() + blocks_per_slice - 1) / blocks_per_slice);
+  const int64_t tile = p->set->weight_edges;
+  const int64_t edge_tiles = std::max<int64_t>(1, (n + tile - 1) / tile);
   const int64_t s0 = std::min(want, edge_tiles);
-  const int64_t per = ((edge_tiles + s0 - 1) / s0) * kWeightEdges;
+  const int64_t per = ((edge_tiles + s0 - 1) / s0) * tile;
   *per_slice = per;
   *slices = (int)std::max<int64_t>(1, (n + per - 1) / per);
 }

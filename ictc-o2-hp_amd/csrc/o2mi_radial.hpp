@@ -65,13 +65,12 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kEdgesPerWave = 16;
 constexpr int kEdgesPerBlock = kEdgesPerWave * kWaves;
-constexpr int kWeightEdges = 32;  // edges per staged tile of the affine-adjoint kernel
 constexpr uint32_t kIdle = 0x80000000u;
 constexpr int kRsrcFlags = 0x00020000;
 
 template <int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
-  [&]<int... I>(std::integer_sequence<int, I...>) {
+  [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
     (f(std::integral_constant<int, I>{}), ...);
   }(std::make_integer_sequence<int, N>{});
 }
@@ -432,11 +431,12 @@ __global__ __launch_bounds__(kThreads, 1) void radial_backward_kernel(Args a, co
   });
 }
 
-// Staged tile of the affine-adjoint kernel: kWeightEdges edges of x and g
+// Staged tile of the affine-adjoint kernel: Plan::kWeightEdges edges of x and g
 // (this block's 16 channels), y and hidden.  Row strides are odd / 16 mod 32
 // so the per-step LDS reads of 4 edges x 16 channels do not collide in banks.
-template <class Plan, int KH>
+template <class Plan, int KH, int NT = kThreads>
 struct WTile {
+  static constexpr int kWeightEdges = Plan::kWeightEdges;
   static constexpr int kXS = 16 * Plan::kComps1 + 1;
   static constexpr int kYS = Plan::kComps2;
   static constexpr int kHS = Geom<KH>::kHid + 16;
@@ -445,15 +445,16 @@ struct WTile {
   static constexpr int kH = kWeightEdges * kHS;
   static constexpr int kFloats = 2 * kX + kY + kH;
   // Per-thread staging registers: ceil(elements / threads) per part.
-  static constexpr int kXPer = (kWeightEdges * 16 * Plan::kComps1 + kThreads - 1) / kThreads;
-  static constexpr int kYPer = (kY + kThreads - 1) / kThreads;
-  static constexpr int kHPer = (kWeightEdges * Geom<KH>::kHid + kThreads - 1) / kThreads;
+  static constexpr int kXPer = (kWeightEdges * 16 * Plan::kComps1 + NT - 1) / NT;
+  static constexpr int kYPer = (kY + NT - 1) / NT;
+  static constexpr int kHPer = (kWeightEdges * Geom<KH>::kHid + NT - 1) / NT;
 };
 
-template <class Plan, int KH>
+template <class Plan, int KH, int NT = kThreads>
 struct WPrefetch {
-  float x[WTile<Plan, KH>::kXPer], g[WTile<Plan, KH>::kXPer];
-  float y[WTile<Plan, KH>::kYPer], h[WTile<Plan, KH>::kHPer];
+  using T = WTile<Plan, KH, NT>;
+  float x[T::kXPer], g[T::kXPer];
+  float y[T::kYPer], h[T::kHPer];
 };
 
 // Element idx of the x/g part of a tile: edge idx / (16 NC), then the
@@ -487,12 +488,13 @@ __device__ __forceinline__ uint32_t tile_row_off(const Args& a, int64_t rows_of_
   return (id >= 0 && id < a.x_rows) ? (uint32_t)id * (uint32_t)a.W1 * 4u : kIdle;
 }
 
-template <class Plan, int KH>
-__device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH>& pf, const Args& a,
+template <class Plan, int KH, int NT = kThreads>
+__device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH, NT>& pf, const Args& a,
                                              const float* gout, int64_t t0, int64_t t_end,
                                              int u0, int64_t rows_of_tile) {
-  using T = WTile<Plan, KH>;
+  using T = WTile<Plan, KH, NT>;
   constexpr int XE = 16 * Plan::kComps1;
+  constexpr int kWeightEdges = Plan::kWeightEdges;
   const int64_t rows = t_end - t0 < kWeightEdges ? t_end - t0 : kWeightEdges;
   const auto rx = x_rsrc(a, t0, rows);
   const auto rg = rows_rsrc(gout, t0, a.W1, rows);
@@ -503,7 +505,7 @@ __device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH>& pf, const Args
   uint32_t voff[T::kXPer], xoff[T::kXPer];
   static_for<T::kXPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     voff[k] = xoff[k] = kIdle;
     if (idx < kWeightEdges * XE) {
       const int edge = idx / XE;
@@ -525,29 +527,30 @@ __device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH>& pf, const Args
   });
   static_for<T::kYPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     pf.y[k] = ld1(ry, idx < T::kY ? (uint32_t)idx * 4u : kIdle);  // rows of y are contiguous
   });
   static_for<T::kHPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     const int edge = idx / Geom<KH>::kHid, h = idx - edge * Geom<KH>::kHid;
     const bool ok = idx < kWeightEdges * Geom<KH>::kHid && h < a.H;
     pf.h[k] = ld1(rh, ok ? (uint32_t)(edge * a.H + h) * 4u : kIdle);
   });
 }
 
-template <class Plan, int KH>
-__device__ __forceinline__ void weight_commit(const WPrefetch<Plan, KH>& pf, float* buf) {
-  using T = WTile<Plan, KH>;
+template <class Plan, int KH, int NT = kThreads>
+__device__ __forceinline__ void weight_commit(const WPrefetch<Plan, KH, NT>& pf, float* buf) {
+  using T = WTile<Plan, KH, NT>;
   constexpr int XE = 16 * Plan::kComps1;
+  constexpr int kWeightEdges = Plan::kWeightEdges;
   float* sx = buf;
   float* sg = buf + T::kX;
   float* sy = buf + 2 * T::kX;
   float* sh = sy + T::kY;
   static_for<T::kXPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     if (idx < kWeightEdges * XE) {
       const int edge = idx / XE, rest = idx - edge * XE;
       sx[edge * T::kXS + rest] = pf.x[k];
@@ -556,12 +559,12 @@ __device__ __forceinline__ void weight_commit(const WPrefetch<Plan, KH>& pf, flo
   });
   static_for<T::kYPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     if (idx < T::kY) sy[idx] = pf.y[k];
   });
   static_for<T::kHPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * kThreads;
+    const int idx = threadIdx.x + k * NT;
     if (idx < kWeightEdges * Geom<KH>::kHid) {
       const int edge = idx / Geom<KH>::kHid, h = idx - edge * Geom<KH>::kHid;
       sh[edge * T::kHS + h] = pf.h[k];
@@ -569,16 +572,18 @@ __device__ __forceinline__ void weight_commit(const WPrefetch<Plan, KH>& pf, flo
   });
 }
 
-// Grid (slices, C/16).  part_alpha: [slices][P*C][H]; part_bias: [slices][P*C].
-template <class Plan, int KH>
-__global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
-    Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
+// dalpha / dbias partials of paths [P0, P0 + NP) over one edge slice and one
+// channel tile; wave w owns the paths P0 + w (mod 8).
+template <class Plan, int KH, int P0, int NP>
+__device__ __forceinline__ void weight_body(float* s_mem, const Args& a, const float* gout,
+                                            int64_t edges_per_slice, float* part_alpha,
+                                            float* part_bias) {
   using G = Geom<KH>;
   using T = WTile<Plan, KH>;
   constexpr int P = Plan::kPaths;
-  constexpr int NPW = (P + kWaves - 1) / kWaves;
+  constexpr int kWeightEdges = Plan::kWeightEdges;
+  constexpr int NPW = (NP + kWaves - 1) / kWaves;
   constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
-  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
   float* s_coef = s_mem;
   float* s_tile = s_mem + kCoefPad;
 
@@ -643,10 +648,10 @@ __global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
       static_for<G::kTiles>([&](auto tc) {
         hv[decltype(tc)::value] = sh[edge * T::kHS + 16 * decltype(tc)::value + j];
       });
-      static_for<P>([&](auto pc) {
-        constexpr int p = decltype(pc)::value;
-        constexpr int q = p / kWaves;
-        if (wave == p % kWaves) {
+      static_for<NP>([&](auto pc) {
+        constexpr int p = P0 + decltype(pc)::value;
+        constexpr int q = decltype(pc)::value / kWaves;
+        if (wave == decltype(pc)::value % kWaves) {
           constexpr RPath ps = Plan::paths[p];
           constexpr REntry X = Plan::e1[ps.i];
           constexpr REntry Y = Plan::e2[ps.j];
@@ -673,10 +678,10 @@ __global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
   const int64_t PC = (int64_t)P * a.C;
   float* pa = part_alpha + (int64_t)blockIdx.x * PC * a.H;
   float* pb = part_bias + (int64_t)blockIdx.x * PC;
-  static_for<P>([&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    constexpr int q = p / kWaves;
-    if (wave == p % kWaves) {
+  static_for<NP>([&](auto pc) {
+    constexpr int p = P0 + decltype(pc)::value;
+    constexpr int q = decltype(pc)::value / kWaves;
+    if (wave == decltype(pc)::value % kWaves) {
       const int64_t row = (int64_t)p * a.C + u0 + j;
       static_for<G::kTiles>([&](auto tc) {
         constexpr int tt = decltype(tc)::value;
@@ -689,6 +694,17 @@ __global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
       if (g == 0) pb[row] = b;
     }
   });
+}
+
+// Grid (slices, C/16).  part_alpha: [slices][P*C][H]; part_bias: [slices][P*C].
+template <class Plan, int KH>
+__global__ __launch_bounds__(kThreads, 1) void radial_weight_kernel(
+    Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
+  using T = WTile<Plan, KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
+  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
+  weight_body<Plan, KH, 0, P>(s_mem, a, gout, edges_per_slice, part_alpha, part_bias);
 }
 
 }  // namespace radial

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "o2mi_radial.hpp"
+#include "o2mi_radial_streamed.hpp"
 
 namespace o2mi {
 namespace radial {
@@ -13,6 +14,8 @@ struct KernelSet {
   int comps1;   // components per channel of the first input
   int comps2;   // width of the second input (V = 1)
   int kh;       // hidden width supported: <= 4 * kh
+  int weight_edges;   // edges per staged tile of the affine-adjoint kernel
+  int weight_groups;  // path groups (grid z) of the affine-adjoint kernel
   hipError_t (*forward)(const Args&, float* out, hipStream_t);
   hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, float* ghid,
                          int needed, hipStream_t);
@@ -26,30 +29,55 @@ inline unsigned edge_blocks(int64_t n) {
 
 template <class Plan, int KH>
 hipError_t launch_forward(const Args& a, float* out, hipStream_t s) {
-  hipLaunchKernelGGL((radial_forward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads), 0,
-                     s, a, out);
+  if constexpr (Plan::kStreamed)
+    hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH>),
+                       dim3((unsigned)((a.n + kEdgesPerWave * kSFwdWaves - 1) /
+                                       (kEdgesPerWave * kSFwdWaves))),
+                       dim3(64 * kSFwdWaves), 0, s, a, out);
+  else
+    hipLaunchKernelGGL((radial_forward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads),
+                       0, s, a, out);
   return hipGetLastError();
 }
 
 template <class Plan, int KH>
 hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* gy, float* ghid,
                            int needed, hipStream_t s) {
-  hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads),
-                     0, s, a, gout, gx, gy, ghid, needed);
+  if constexpr (Plan::kStreamed)
+    hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH>),
+                       dim3((unsigned)((a.n + kEdgesPerWave * kSBwdWaves - 1) /
+                                       (kEdgesPerWave * kSBwdWaves))),
+                       dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, ghid, needed);
+  else
+    hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)),
+                       dim3(kThreads), 0, s, a, gout, gx, gy, ghid, needed);
   return hipGetLastError();
 }
 
 template <class Plan, int KH>
 hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_slice, int slices,
                          float* part_alpha, float* part_bias, hipStream_t s) {
-  hipLaunchKernelGGL((radial_weight_kernel<Plan, KH>), dim3((unsigned)slices, (unsigned)(a.C / 16)),
-                     dim3(kThreads), 0, s, a, gout, edges_per_slice, part_alpha, part_bias);
+  if constexpr (Plan::kStreamed)
+    hipLaunchKernelGGL((radial_weight_streamed_kernel<Plan, KH>),
+                       dim3((unsigned)slices, (unsigned)(a.C / 16), wgt_groups<Plan>()),
+                       dim3(64 * kSWgtWaves), 0, s, a, gout, edges_per_slice, part_alpha,
+                       part_bias);
+  else
+    hipLaunchKernelGGL((radial_weight_kernel<Plan, KH>), dim3((unsigned)slices, (unsigned)(a.C / 16)),
+                       dim3(kThreads), 0, s, a, gout, edges_per_slice, part_alpha, part_bias);
   return hipGetLastError();
+}
+
+template <class Plan>
+constexpr int weight_groups() {
+  if constexpr (Plan::kStreamed) return wgt_groups<Plan>();
+  else return 1;
 }
 
 template <class Plan, int KH>
 const KernelSet* kernel_set() {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
+                                Plan::kWeightEdges, weight_groups<Plan>(),
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>};
   return &set;

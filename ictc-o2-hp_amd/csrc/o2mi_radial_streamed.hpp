@@ -1,0 +1,583 @@
+// Streamed radial kernels: structures whose alpha tile of every path does
+// not fit LDS (RadialUvuTensorProduct with m_max 6 and a full first input has
+// 254 paths: 254 x 16 channels x 64 hidden floats = 1 MiB per channel tile).
+//
+// Same lane mapping and MFMA weight tiles as radial_forward_kernel /
+// radial_backward_kernel, with two changes:
+//  * alpha and bias are staged in chunks of Plan::kChunk paths, double
+//    buffered: the global loads of chunk c + 1 are in flight while chunk c is
+//    consumed, and land in the other LDS buffer before the chunk barrier.  The
+//    chunk sequence runs on across channel tiles.
+//  * paths are walked grouped by output entry (forward: one output entry of
+//    accumulators live) or by first-input entry (input adjoints: one x and one
+//    dx entry live, the next x entry loaded a group ahead), so the per-lane
+//    state is one full row (4 channels x components) plus one entry.
+// The affine-parameter adjoints use radial_weight_kernel with path groups.
+#pragma once
+
+#include "o2mi_radial.hpp"
+
+namespace o2mi {
+namespace radial {
+
+// Waves per block.  The forward's per-lane state (a full x row of 4 channels
+// x components, one output entry, the hidden operand) fits the 256 registers
+// of two waves per SIMD.  The input adjoints add the weight-adjoint and hidden
+// accumulators and need one wave per SIMD (512 registers).
+constexpr int kSFwdWaves = 8;
+constexpr int kSBwdWaves = 4;
+
+template <class Plan, int KH>
+struct SLayout {
+  static constexpr int kChunk = Plan::kChunk;
+  static constexpr int kCoef = 0;
+  static constexpr int kBuf0 = (Plan::kPaths * 8 + 3) / 4 * 4;
+  static constexpr int kBias = 0;                  // within a buffer: [kChunk][16]
+  static constexpr int kAlpha = kChunk * 16;       // within a buffer: [kChunk * 16][kRow]
+  static constexpr int kBufFloats = kAlpha + kChunk * 16 * Geom<KH>::kRow;
+  static constexpr int kFloats = kBuf0 + 2 * kBufFloats;
+  static constexpr int kChunks = (Plan::kPaths + kChunk - 1) / kChunk;
+  static_assert(kAlpha % 4 == 0 && kBufFloats % 4 == 0, "buffers must be 16-byte aligned");
+};
+
+// Per-thread registers of one chunk in flight: alpha rows as float4 (hidden
+// zero-padded) and one bias value.
+template <class Plan, int KH, int NT>
+struct SChunk {
+  static constexpr int kVec = Geom<KH>::kHid / 4;   // float4 per alpha row
+  static constexpr int kPerPath = 16 * kVec;        // float4 per path and channel tile
+  static_assert(NT % kPerPath == 0, "a thread's float4 must stay in one path slot");
+  static constexpr int kSlotsPerPass = NT / kPerPath;
+  static constexpr int kPer = (Plan::kChunk * kPerPath + NT - 1) / NT;
+  f4 alpha[kPer];
+  float bias;
+};
+
+// Path at traversal position q (Order = Plan::fwd or Plan::bwd).
+template <class Plan, bool kBwd>
+constexpr int path_at(int q) {
+  return kBwd ? Plan::bwd[q] : Plan::fwd[q];
+}
+
+// Global loads of chunk c (positions c*kChunk ...) for channel tile u0.
+template <class Plan, int KH, int NT, bool kBwd, int c>
+__device__ __forceinline__ void chunk_fetch(SChunk<Plan, KH, NT>& pf, const Args& a, int u0) {
+  using S = SChunk<Plan, KH, NT>;
+  constexpr int PC = Plan::kChunk;
+  // Laundered: the slot -> path selects of every chunk depend only on the
+  // thread and would otherwise be hoisted out of the channel loop (and spill).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  static_for<S::kPer>([&](auto kc) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value;
+    const int sub = tid / S::kPerPath;           // slot within this pass
+    const int rest = tid - sub * S::kPerPath;    // r * kVec + qv
+    const int r = rest / S::kVec, qv = rest - r * S::kVec;
+    int path = -1;
+    static_for<S::kSlotsPerPass>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int slot = k * S::kSlotsPerPass + decltype(sc)::value;
+      constexpr int pos = c * PC + slot;
+      if constexpr (slot < PC && pos < Plan::kPaths)
+        if (sub == decltype(sc)::value) path = path_at<Plan, kBwd>(pos);
+    });
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (path >= 0 && 4 * qv < a.H)
+      v = *reinterpret_cast<const f4*>(a.alpha + (int64_t)(path * a.C + u0 + r) * a.H + 4 * qv);
+    pf.alpha[k] = v;
+  });
+  pf.bias = 0.f;
+  if (a.bias && tid < PC * 16) {
+    const int slot = tid >> 4;
+    int path = -1;
+    static_for<PC>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int pos = c * PC + decltype(sc)::value;
+      if constexpr (pos < Plan::kPaths)
+        if (slot == decltype(sc)::value) path = path_at<Plan, kBwd>(pos);
+    });
+    if (path >= 0) pf.bias = a.bias[path * a.C + u0 + (tid & 15)];
+  }
+}
+
+template <class Plan, int KH, int NT>
+__device__ __forceinline__ void chunk_commit(const SChunk<Plan, KH, NT>& pf, float* buf) {
+  using S = SChunk<Plan, KH, NT>;
+  using G = Geom<KH>;
+  using L = SLayout<Plan, KH>;
+  const int tid = threadIdx.x;
+  static_for<S::kPer>([&](auto kc) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = tid + k * NT;
+    if (idx < Plan::kChunk * S::kPerPath) {
+      const int row = idx / S::kVec, qv = idx - row * S::kVec;   // row = slot * 16 + r
+      *reinterpret_cast<f4*>(buf + L::kAlpha + row * G::kRow + 4 * qv) = pf.alpha[k];
+    }
+  });
+  if (tid < Plan::kChunk * 16) buf[L::kBias + tid] = pf.bias;
+}
+
+// Whether first-input entry e is the output (kOut) or first input (!kOut)
+// of some path.
+template <class Plan, bool kOut>
+constexpr bool entry_used(int e) {
+  for (int p = 0; p < Plan::kPaths; ++p)
+    if ((kOut ? Plan::paths[p].k : Plan::paths[p].i) == e) return true;
+  return false;
+}
+
+template <int Dim>
+__device__ __forceinline__ void store_zero_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off,
+                                                 int off_c, int u) {
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  store_entry<Dim>(r, row_off, off_c, u, z);
+}
+
+template <class Plan, int KH>
+__global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_kernel(Args a,
+                                                                                   float* out) {
+  constexpr int NT = 64 * kSFwdWaves;
+  using G = Geom<KH>;
+  using L = SLayout<Plan, KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int NC = Plan::kComps1;
+  constexpr int PC = Plan::kChunk;
+  constexpr int NCH = L::kChunks;
+  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int64_t e0 = ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
+  const auto rx = x_rsrc(a, e0, rows);
+  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
+  const auto ro = rows_rsrc(out, e0, a.W1, rows);
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (out)
+  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
+  float hid[KH];
+  load_hidden<KH>(rh, a.H, g, j, hid);
+  float yv[Plan::kComps2];
+  static_for<Plan::kComps2>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
+  });
+
+  SChunk<Plan, KH, NT> pf;
+  chunk_fetch<Plan, KH, NT, false, 0>(pf, a, 0);
+  chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  int parity = 0;  // LDS buffer of the current chunk
+  for (int u0 = 0; u0 < a.C; u0 += 16) {
+    __syncthreads();
+    const int u = u0 + 4 * g;
+    float xv[4 * NC];
+    load_row<Plan>(rx, xsrc, a.C, u, xv);
+    static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec)::value;
+      constexpr REntry O = Plan::e1[e];
+      if constexpr (!entry_used<Plan, true>(e)) store_zero_entry<O.dim>(ro, xrow, O.off * a.C, u);
+    });
+    float ov[8];
+    static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
+      constexpr int c = decltype(cc)::value;
+      if constexpr (c + 1 < NCH) {
+        chunk_fetch<Plan, KH, NT, false, c + 1>(pf, a, u0);
+      } else {
+        if (u0 + 16 < a.C) chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u0 + 16);
+      }
+      const int buf = L::kBuf0 + parity * L::kBufFloats;
+      // Laundered per chunk so that neither addresses nor the uniform
+      // coupling reads are hoisted into registers across chunks.
+      int coef_off = L::kCoef, bias_off = buf + L::kBias + 4 * g;
+      int arow_off = buf + L::kAlpha + j * G::kRow + KH * g;
+      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off));
+      const float* cf = s_mem + coef_off;
+      static_for<(P - c * PC < PC ? P - c * PC : PC)>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int slot = decltype(sc)::value;
+        constexpr int q = c * PC + slot;
+        constexpr int p = Plan::fwd[q];
+        constexpr RPath ps = Plan::paths[p];
+        constexpr REntry X = Plan::e1[ps.i];
+        constexpr REntry Y = Plan::e2[ps.j];
+        constexpr REntry O = Plan::e1[ps.k];
+        constexpr bool first = q == 0 || Plan::paths[Plan::fwd[q == 0 ? 0 : q - 1]].k != ps.k;
+        constexpr bool last = q == P - 1 || Plan::paths[Plan::fwd[q == P - 1 ? q : q + 1]].k != ps.k;
+        if constexpr (first) static_for<8>([&](auto ic) __attribute__((always_inline)) { ov[decltype(ic)::value] = 0.f; });
+        const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        static_for<8>([&](auto sc2) __attribute__((always_inline)) {
+          constexpr int sl = decltype(sc2)::value;
+          constexpr int oc = sl >> 2, ia = (sl >> 1) & 1, ib = sl & 1;
+          if constexpr ((ps.mask >> sl) & 1) {
+            const float cy = cf[p * 8 + sl] * yv[Y.base + ib];
+            static_for<4>([&](auto rc) __attribute__((always_inline)) {
+              constexpr int r = decltype(rc)::value;
+              ov[r * O.dim + oc] += cy * (xv[4 * X.base + r * X.dim + ia] * w[r]);
+            });
+          }
+        });
+        // Pinned per path: left alone, the compiler sinks the accumulation
+        // chain towards the entry's store and keeps every product live.
+#pragma unroll
+        for (int i = 0; i < 4 * O.dim; ++i) asm volatile("" : "+v"(ov[i]));
+        if constexpr (last) store_entry<O.dim>(ro, xrow, O.off * a.C, u, ov);
+      });
+      if (c + 1 < NCH || u0 + 16 < a.C)
+        chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
+      parity ^= 1;
+      __syncthreads();
+    });
+  }
+}
+
+// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here).
+template <class Plan, int KH>
+__global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_kernel(
+    Args a, const float* gout, float* gx, float* gy, float* ghid, int needed) {
+  constexpr int NT = 64 * kSBwdWaves;
+  using G = Geom<KH>;
+  using L = SLayout<Plan, KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int NC = Plan::kComps1;
+  constexpr int NY = Plan::kComps2;
+  constexpr int PC = Plan::kChunk;
+  constexpr int NCH = L::kChunks;
+  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int64_t e0 = ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
+  const auto rx = x_rsrc(a, e0, rows);
+  const auto rg = rows_rsrc(gout, e0, a.W1, rows);
+  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
+  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (g, dx)
+  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
+  const bool need_y = (needed & 2) != 0;
+  const auto rdx = rows_rsrc(gx, e0, a.W1, (needed & 1) ? rows : 0);
+  const auto rgh = rows_rsrc(ghid, e0, a.H, (needed & 4) ? rows : 0);
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
+  float hid[KH];
+  load_hidden<KH>(rh, a.H, g, j, hid);
+  float yv[NY], dyv[NY];
+  static_for<NY>([&](auto cc) __attribute__((always_inline)) {
+    constexpr int c = decltype(cc)::value;
+    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
+    dyv[c] = 0.f;
+  });
+  f4 gh[G::kTiles];
+  static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) { gh[decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
+
+  SChunk<Plan, KH, NT> pf;
+  chunk_fetch<Plan, KH, NT, true, 0>(pf, a, 0);
+  chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  int parity = 0;
+  for (int u0 = 0; u0 < a.C; u0 += 16) {
+    __syncthreads();
+    const int u = u0 + 4 * g;
+    float gv[4 * NC];
+    load_row<Plan>(rg, xrow, a.C, u, gv);
+    static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec)::value;
+      constexpr REntry X = Plan::e1[e];
+      if constexpr (!entry_used<Plan, false>(e)) store_zero_entry<X.dim>(rdx, xrow, X.off * a.C, u);
+    });
+    // x entry of the current first-input group, and of the next one (loaded a
+    // group ahead of its use).
+    float xc[8], xn[8], dxc[8];
+    {
+      constexpr REntry X0 = Plan::e1[Plan::paths[Plan::bwd[0]].i];
+      load_entry<X0.dim>(rx, xsrc, X0.off * a.C, u, xn);
+    }
+    static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
+      constexpr int c = decltype(cc)::value;
+      if constexpr (c + 1 < NCH) {
+        chunk_fetch<Plan, KH, NT, true, c + 1>(pf, a, u0);
+      } else {
+        if (u0 + 16 < a.C) chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u0 + 16);
+      }
+      const int buf = L::kBuf0 + parity * L::kBufFloats;
+      int coef_off = L::kCoef, bias_off = buf + L::kBias + 4 * g;
+      int arow_off = buf + L::kAlpha + j * G::kRow + KH * g;
+      int acol_off = buf + L::kAlpha + 4 * g * G::kRow + j;
+      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off));
+      const float* cf = s_mem + coef_off;
+      static_for<(P - c * PC < PC ? P - c * PC : PC)>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int slot = decltype(sc)::value;
+        constexpr int q = c * PC + slot;
+        constexpr int p = Plan::bwd[q];
+        constexpr RPath ps = Plan::paths[p];
+        constexpr REntry X = Plan::e1[ps.i];
+        constexpr REntry Y = Plan::e2[ps.j];
+        constexpr REntry O = Plan::e1[ps.k];
+        constexpr bool first = q == 0 || Plan::paths[Plan::bwd[q == 0 ? 0 : q - 1]].i != ps.i;
+        constexpr bool last = q == P - 1 || Plan::paths[Plan::bwd[q == P - 1 ? q : q + 1]].i != ps.i;
+        if constexpr (first) {
+          static_for<8>([&](auto ic) __attribute__((always_inline)) {
+            xc[decltype(ic)::value] = xn[decltype(ic)::value];
+            dxc[decltype(ic)::value] = 0.f;
+          });
+          if constexpr (q < P - 1) {
+            // First position of the next group.
+            constexpr int qn = [] {
+              int t = q + 1;
+              while (t < P && Plan::paths[Plan::bwd[t]].i == Plan::paths[Plan::bwd[q]].i) ++t;
+              return t;
+            }();
+            if constexpr (qn < P) {
+              constexpr REntry XN = Plan::e1[Plan::paths[Plan::bwd[qn]].i];
+              load_entry<XN.dim>(rx, xsrc, XN.off * a.C, u, xn);
+            }
+          }
+        }
+        const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        float gw[4] = {0.f, 0.f, 0.f, 0.f};
+        static_for<8>([&](auto sc2) __attribute__((always_inline)) {
+          constexpr int sl = decltype(sc2)::value;
+          constexpr int oc = sl >> 2, ia = (sl >> 1) & 1, ib = sl & 1;
+          if constexpr ((ps.mask >> sl) & 1) {
+            const float cfv = cf[p * 8 + sl];
+            const float cy = cfv * yv[Y.base + ib];
+            static_for<4>([&](auto rc) __attribute__((always_inline)) {
+              constexpr int r = decltype(rc)::value;
+              const float xr = xc[r * X.dim + ia];
+              const float gr = gv[4 * O.base + r * O.dim + oc];
+              gw[r] += cy * (xr * gr);
+              dyv[Y.base + ib] += cfv * (xr * gr) * w[r];
+              dxc[r * X.dim + ia] += cy * (gr * w[r]);
+            });
+          }
+        });
+        // Pinned per path (see the forward): an unpinned dy chain is sunk to
+        // the end of the channel tile with all its products live.
+        asm volatile("" : "+v"(dyv[Y.base]));
+        if constexpr (Y.dim == 2) asm volatile("" : "+v"(dyv[Y.base + 1]));
+        const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
+        static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+          constexpr int t = decltype(tc)::value;
+          gh[t] = mfma(acol[16 * t], gw[0], gh[t]);
+          gh[t] = mfma(acol[G::kRow + 16 * t], gw[1], gh[t]);
+          gh[t] = mfma(acol[2 * G::kRow + 16 * t], gw[2], gh[t]);
+          gh[t] = mfma(acol[3 * G::kRow + 16 * t], gw[3], gh[t]);
+        });
+        if constexpr (last) store_entry<X.dim>(rdx, xrow, X.off * a.C, u, dxc);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if (c + 1 < NCH || u0 + 16 < a.C)
+        chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
+      parity ^= 1;
+      __syncthreads();
+    });
+  }
+  if (need_y) {
+    // Lanes j, j+16, j+32, j+48 hold the channel partial sums of edge j.
+    static_for<NY>([&](auto cc) __attribute__((always_inline)) {
+      constexpr int c = decltype(cc)::value;
+      dyv[c] += __shfl_xor(dyv[c], 16);
+      dyv[c] += __shfl_xor(dyv[c], 32);
+    });
+    if (g == 0 && j < rows) {
+      float* dst = gy + (e0 + j) * a.W2;
+      static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
+    }
+  }
+  static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value;
+    const int h = 16 * t + 4 * g;
+    st4(rgh, gh[t], h < a.H ? (uint32_t)(j * a.H + h) * 4u : kIdle);
+  });
+}
+
+// Affine-parameter adjoints of a streamed structure (dalpha = gw^T hidden,
+// dbias = sum_e gw).  Same staged tiles as radial_weight_kernel, but one wave
+// per SIMD owning 16 consecutive paths of Plan::wgt (grouped by second-input
+// entry): its dalpha tiles, 16 paths x 64 hidden x 16 channels, sit in the
+// accumulator registers, and per step it reads from LDS only the operand
+// components its paths use (about half of them).
+constexpr int kSWgtWaves = 4;
+constexpr int kSWgtPaths = 16;                      // paths per wave
+constexpr int kSWgtGroup = kSWgtWaves * kSWgtPaths;  // paths per block (grid z)
+
+template <class Plan>
+constexpr int wgt_groups() {
+  return (Plan::kPaths + kSWgtGroup - 1) / kSWgtGroup;
+}
+
+// Whether a path at positions [q0, q0 + n) of Plan::wgt uses entry e as its
+// first input (role 0), second input (1) or output (2).
+template <class Plan, int Role>
+constexpr bool wgt_uses(int q0, int n, int e) {
+  for (int q = q0; q < q0 + n && q < Plan::kPaths; ++q) {
+    const RPath ps = Plan::paths[Plan::wgt[q]];
+    if ((Role == 0 ? ps.i : Role == 1 ? ps.j : ps.k) == e) return true;
+  }
+  return false;
+}
+
+template <class Plan, int KH, int Q0, int NPW>
+__device__ __forceinline__ void wgt_step(const float* buf, const float* cf, int edge, int j,
+                                         f4 (&ga)[kSWgtPaths][Geom<KH>::kTiles],
+                                         float (&gb)[kSWgtPaths]) {
+  using G = Geom<KH>;
+  using T = WTile<Plan, KH, 64 * kSWgtWaves>;
+  const float* sx = buf;
+  const float* sg = buf + T::kX;
+  const float* sy = buf + 2 * T::kX;
+  const float* sh = sy + T::kY;
+  float xv[Plan::kComps1], gv[Plan::kComps1], yv[Plan::kComps2], hv[G::kTiles];
+  static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
+    constexpr int e = decltype(ec)::value;
+    constexpr REntry E = Plan::e1[e];
+    constexpr bool use_x = wgt_uses<Plan, 0>(Q0, NPW, e);
+    constexpr bool use_g = wgt_uses<Plan, 2>(Q0, NPW, e);
+    static_for<E.dim>([&](auto dc) __attribute__((always_inline)) {
+      constexpr int d = decltype(dc)::value;
+      const int o = edge * T::kXS + 16 * E.base + j * E.dim + d;
+      if constexpr (use_x) xv[E.base + d] = sx[o];
+      if constexpr (use_g) gv[E.base + d] = sg[o];
+    });
+  });
+  static_for<Plan::kEntries2>([&](auto ec) __attribute__((always_inline)) {
+    constexpr int e = decltype(ec)::value;
+    constexpr REntry E = Plan::e2[e];
+    if constexpr (wgt_uses<Plan, 1>(Q0, NPW, e))
+      static_for<E.dim>([&](auto dc) __attribute__((always_inline)) {
+        constexpr int d = decltype(dc)::value;
+        yv[E.base + d] = sy[edge * T::kYS + E.base + d];
+      });
+  });
+  static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+    hv[decltype(tc)::value] = sh[edge * T::kHS + 16 * decltype(tc)::value + j];
+  });
+  static_for<NPW>([&](auto qc) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    constexpr int p = Plan::wgt[Q0 + q];
+    constexpr RPath ps = Plan::paths[p];
+    constexpr REntry X = Plan::e1[ps.i];
+    constexpr REntry Y = Plan::e2[ps.j];
+    constexpr REntry O = Plan::e1[ps.k];
+    float gw = 0.f;
+    static_for<8>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int slot = decltype(sc)::value;
+      constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
+      if constexpr ((ps.mask >> slot) & 1)
+        gw += cf[p * 8 + slot] * yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+    });
+    gb[q] += gw;
+    static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int tt = decltype(tc)::value;
+      ga[q][tt] = mfma(hv[tt], gw, ga[q][tt]);
+    });
+  });
+}
+
+template <class Plan, int KH, int G0>
+__device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const float* gout,
+                                         int64_t edges_per_slice, float* part_alpha,
+                                         float* part_bias) {
+  constexpr int NT = 64 * kSWgtWaves;
+  using G = Geom<KH>;
+  using T = WTile<Plan, KH, NT>;
+  constexpr int P = Plan::kPaths;
+  constexpr int kWeightEdges = Plan::kWeightEdges;
+  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
+  float* s_coef = s_mem;
+  float* s_tile = s_mem + kCoefPad;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int u0 = blockIdx.y * 16;
+  const int64_t begin = (int64_t)blockIdx.x * edges_per_slice;
+  const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
+  const int tiles = end > begin ? (int)((end - begin + kWeightEdges - 1) / kWeightEdges) : 0;
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_coef[idx] = a.coef[idx];
+  f4 ga[kSWgtPaths][G::kTiles];
+  float gb[kSWgtPaths];
+  static_for<kSWgtPaths>([&](auto qc) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    gb[q] = 0.f;
+    static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+      ga[q][decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f};
+    });
+  });
+
+  WPrefetch<Plan, KH, NT> pf;
+  if (tiles > 0) {
+    weight_fetch<Plan, KH, NT>(pf, a, gout, begin, end, u0, tile_rows(a, begin, end));
+    weight_commit<Plan, KH, NT>(pf, s_tile);
+  }
+  int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
+  __syncthreads();
+  for (int t = 0; t < tiles; ++t) {
+    const bool more = t + 1 < tiles;
+    if (more) {
+      const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
+      weight_fetch<Plan, KH, NT>(pf, a, gout, t1, end, u0, next_rows);
+      next_rows = tile_rows(a, t1 + kWeightEdges, end);
+    }
+    const float* buf = s_tile + (t & 1) * T::kFloats;
+#pragma unroll
+    for (int s = 0; s < kWeightEdges / 4; ++s) {
+      int coef_off = 0;
+      asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
+      const float* cf = s_coef + coef_off;
+      static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
+        constexpr int w = decltype(wc)::value;
+        constexpr int q0 = G0 * kSWgtGroup + w * kSWgtPaths;
+        constexpr int np = P - q0 < kSWgtPaths ? P - q0 : kSWgtPaths;
+        if constexpr (np > 0)
+          if (wave == w) wgt_step<Plan, KH, q0, np>(buf, cf, 4 * s + g, j, ga, gb);
+      });
+    }
+    if (more) weight_commit<Plan, KH, NT>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
+    __syncthreads();
+  }
+
+  const int64_t PC = (int64_t)P * a.C;
+  float* pa = part_alpha + (int64_t)blockIdx.x * PC * a.H;
+  float* pb = part_bias + (int64_t)blockIdx.x * PC;
+  static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
+    constexpr int w = decltype(wc)::value;
+    constexpr int q0 = G0 * kSWgtGroup + w * kSWgtPaths;
+    constexpr int np = P - q0 < kSWgtPaths ? P - q0 : kSWgtPaths;
+    if constexpr (np > 0) {
+      if (wave == w) {
+        static_for<np>([&](auto qc) __attribute__((always_inline)) {
+          constexpr int q = decltype(qc)::value;
+          const int64_t row = (int64_t)Plan::wgt[q0 + q] * a.C + u0 + j;
+          static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+            constexpr int tt = decltype(tc)::value;
+            const int h = 16 * tt + 4 * g;
+            if (h < a.H) *reinterpret_cast<f4*>(pa + row * a.H + h) = ga[q][tt];
+          });
+          float b = gb[q];
+          b += __shfl_xor(b, 16);
+          b += __shfl_xor(b, 32);
+          if (g == 0) pb[row] = b;
+        });
+      }
+    }
+  });
+}
+
+// Grid (slices, C/16, wgt_groups<Plan>()).
+template <class Plan, int KH>
+__global__ __launch_bounds__(64 * kSWgtWaves, 1) void radial_weight_streamed_kernel(
+    Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
+  using T = WTile<Plan, KH, 64 * kSWgtWaves>;
+  constexpr int kCoefPad = (Plan::kPaths * 8 + 3) / 4 * 4;
+  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
+  static_for<wgt_groups<Plan>()>([&](auto gc) __attribute__((always_inline)) {
+    constexpr int grp = decltype(gc)::value;
+    if (blockIdx.z == grp)
+      wgt_body<Plan, KH, grp>(s_mem, a, gout, edges_per_slice, part_alpha, part_bias);
+  });
+}
+
+}  // namespace radial
+}  // namespace o2mi

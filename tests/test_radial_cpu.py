@@ -129,7 +129,11 @@ def test_radial_plan_create_validation():
     assert lib.o2mi_radial_plan_create(24, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -2
     assert lib.o2mi_radial_plan_create(64, 4, 0, 4, 0, 66, ctypes.byref(handle)) == -2
     assert lib.o2mi_radial_plan_create(64, 4, 0, 4, 0, 128, ctypes.byref(handle)) == -2
-    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 0, 64, ctypes.byref(handle)) == -2
+    # m_max 6, full / canonical: 254 paths, streamed kernels.
+    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 0, 64, ctypes.byref(handle)) == 0
+    assert lib.o2mi_radial_paths(handle) == 254
+    assert lib.o2mi_radial_plan_destroy(handle) == 0
+    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 1, 64, ctypes.byref(handle)) == -2
     assert lib.o2mi_radial_plan_create(0, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_plan_create(64, 4, 2, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_backward_workspace_bytes(None, 10, 31) == 0

@@ -89,10 +89,46 @@ def test_fused_structures(c, m, parity, parity_in2, hidden, kw):
     assert radial_ops.fused_plan(tp._kernel_metadata_id, hidden) is not None
 
 
+# The reference's radial benchmark structure (m_max 6, full first input,
+# canonical angular input, 254 paths): streamed kernels, alpha staged in
+# chunks; the affine adjoints run in 4 path groups.
+STREAMED = [
+    (16, 64, 300, True, {}),
+    (32, 48, 129, False, {"path_normalization": "path"}),
+    (64, 64, 65, True, {"normalization": "norm"}),
+    (48, 20, 1, True, {}),
+]
+
+
+@pytest.mark.parametrize("c,hidden,n,bias,kw", STREAMED)
+def test_streamed_structure(c, hidden, n, bias, kw):
+    from ictc_o2_hp import radial_ops
+    tp, _ = _case(c, 6, "full", "canonical", hidden, n, bias=bias, seed=c + n, **kw)
+    assert radial_ops.fused_plan(tp._kernel_metadata_id, hidden) is not None
+
+
+@pytest.mark.parametrize("roles", [("x",), ("y",), ("hidden",), ("alpha",), ("y", "bias")])
+def test_streamed_gradient_roles(roles):
+    _case(16, 6, "full", "canonical", 64, 70, seed=21, roles=roles)
+
+
+def test_streamed_affine_adjoints_reproducible():
+    tp, linear, module, plan = _build(16, 6, "full", "canonical", 64, True, 22)
+    torch.manual_seed(22)
+    x = torch.randn(700, tp.input1_dimension, device="cuda")
+    y = torch.randn(700, tp.input2_dimension, device="cuda")
+    h = torch.randn(700, 64, device="cuda")
+    g = torch.randn(700, tp.input1_dimension, device="cuda")
+    first = torch.autograd.grad(module(x, y, h), (linear.weight, linear.bias), g)
+    second = torch.autograd.grad(module(x, y, h), (linear.weight, linear.bias), g)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
 COMPOSED = [
     (24, 2, "canonical", "canonical", 64, {}),      # C % 16 != 0
     (16, 2, "canonical", "canonical", 6, {}),       # H % 4 != 0
-    (16, 6, "full", "canonical", 64, {}),           # alpha tile larger than LDS
+    (16, 6, "full", "full", 64, {}),                # 508 paths: no kernel compiled
     (16, 2, "canonical", "canonical", 96, {}),      # H > 64
 ]
 
