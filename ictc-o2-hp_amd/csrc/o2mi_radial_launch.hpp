@@ -43,12 +43,12 @@ hipError_t launch_forward(const Args& a, float* out, hipStream_t s) {
 template <class Plan, int KH>
 hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* gy, float* ghid,
                            int needed, hipStream_t s) {
-  if constexpr (Plan::kStreamed)
+  if constexpr (Plan::kStreamed) {
     hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH>),
                        dim3((unsigned)((a.n + kEdgesPerWave * kSBwdWaves - 1) /
                                        (kEdgesPerWave * kSBwdWaves))),
                        dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, ghid, needed);
-  else
+  } else
     hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)),
                        dim3(kThreads), 0, s, a, gout, gx, gy, ghid, needed);
   return hipGetLastError();

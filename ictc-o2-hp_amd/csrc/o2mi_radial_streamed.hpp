@@ -20,12 +20,15 @@
 namespace o2mi {
 namespace radial {
 
-// Waves per block.  The forward's per-lane state (a full x row of 4 channels
-// x components, one output entry, the hidden operand) fits the 256 registers
-// of two waves per SIMD.  The input adjoints add the weight-adjoint and hidden
-// accumulators and need one wave per SIMD (512 registers).
+// Waves per block: two per SIMD (256 registers each).  The input adjoints
+// spill a few registers there (their state adds the hidden-adjoint
+// accumulators and the next x entry), and still run 18% faster than at one
+// wave per SIMD with 512 registers.
 constexpr int kSFwdWaves = 8;
-constexpr int kSBwdWaves = 4;
+#ifndef O2MI_SBWD_WAVES
+#define O2MI_SBWD_WAVES 8
+#endif
+constexpr int kSBwdWaves = O2MI_SBWD_WAVES;
 
 template <class Plan, int KH>
 struct SLayout {
@@ -351,10 +354,12 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
             });
           }
         });
-        // Pinned per path (see the forward): an unpinned dy chain is sunk to
-        // the end of the channel tile with all its products live.
+        // Pinned per path (see the forward): unpinned, the dy and dx chains
+        // are sunk towards their stores with all their products live.
         asm volatile("" : "+v"(dyv[Y.base]));
         if constexpr (Y.dim == 2) asm volatile("" : "+v"(dyv[Y.base + 1]));
+#pragma unroll
+        for (int i = 0; i < 4 * X.dim; ++i) asm volatile("" : "+v"(dxc[i]));
         const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
         static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
           constexpr int t = decltype(tc)::value;
@@ -392,13 +397,20 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
 }
 
 // Affine-parameter adjoints of a streamed structure (dalpha = gw^T hidden,
-// dbias = sum_e gw).  Same staged tiles as radial_weight_kernel, but one wave
-// per SIMD owning 16 consecutive paths of Plan::wgt (grouped by second-input
-// entry): its dalpha tiles, 16 paths x 64 hidden x 16 channels, sit in the
-// accumulator registers, and per step it reads from LDS only the operand
-// components its paths use (about half of them).
-constexpr int kSWgtWaves = 4;
-constexpr int kSWgtPaths = 16;                      // paths per wave
+// dbias = sum_e gw).  Same staged tiles as radial_weight_kernel, but each wave
+// owns 8 consecutive paths of Plan::wgt (grouped by second-input entry): its
+// dalpha tiles, 8 paths x 64 hidden x 16 channels, stay in registers, and per
+// step it reads from LDS only the operand components its paths use (about a
+// third of them).  8 waves of 8 paths: two waves per SIMD, 19% faster than 4
+// waves of 16 paths (one wave per SIMD, half the LDS reads per MFMA).
+#ifndef O2MI_SWGT_WAVES
+#define O2MI_SWGT_WAVES 8
+#endif
+#ifndef O2MI_SWGT_PATHS
+#define O2MI_SWGT_PATHS 8
+#endif
+constexpr int kSWgtWaves = O2MI_SWGT_WAVES;
+constexpr int kSWgtPaths = O2MI_SWGT_PATHS;         // paths per wave
 constexpr int kSWgtGroup = kSWgtWaves * kSWgtPaths;  // paths per block (grid z)
 
 template <class Plan>
