@@ -81,6 +81,42 @@ void slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slic
 
 bool aligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Channels per block of the streamed kernels: all of them, unless the edge
+// blocks alone would leave CUs idle; then the channel tiles are split over
+// grid y (whole 16-channel tiles, no empty split).
+int stream_span(const o2mi_radial_plan* p, int64_t n) {
+  const int per_block = p->set->stream_edges;
+  if (per_block == 0) return p->C;
+  const int64_t blocks = std::max<int64_t>(1, (n + per_block - 1) / per_block);
+  const int64_t cus = device_cus();
+  const int tiles = p->C / 16;
+  if (blocks >= cus || tiles == 1) return p->C;
+  const int64_t want = std::min<int64_t>(tiles, (cus + blocks - 1) / blocks);
+  return 16 * (int)((tiles + want - 1) / want);
+}
+
+int stream_splits(const o2mi_radial_plan* p, int64_t n) {
+  const int span = stream_span(p, n);
+  return (p->C + span - 1) / span;
+}
+
+// Floats of the affine-adjoint slice partials, then of the split dy / dhidden
+// partials, in the backward workspace.
+int64_t weight_part_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
+  if (!(needed & 24) || n <= 0) return 0;
+  int64_t per = 0;
+  int slices = 0;
+  slicing(p, n, &per, &slices);
+  const int64_t rows = (int64_t)p->set->paths * p->C;
+  return (int64_t)slices * (rows * p->H + rows);
+}
+
+int64_t split_part_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
+  const int splits = stream_splits(p, n);
+  if (splits <= 1 || n <= 0) return 0;
+  return (int64_t)splits * n * (((needed & 2) ? p->W2 : 0) + ((needed & 4) ? p->H : 0));
+}
+
 Args make_args(const o2mi_radial_plan* p, int64_t n, const float* x, const float* y,
                const float* hidden, const float* alpha, const float* bias, const float* coef) {
   Args a;
@@ -97,6 +133,9 @@ Args make_args(const o2mi_radial_plan* p, int64_t n, const float* x, const float
   a.coef = coef;
   a.xindex = nullptr;
   a.x_rows = n;
+  a.tile_span = stream_span(p, n);
+  a.part_dy = nullptr;
+  a.part_gh = nullptr;
   return a;
 }
 
@@ -172,21 +211,41 @@ int radial_backward(const o2mi_radial_plan* plan, const Args& a, const float* gr
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
   if ((needed & 8) && !aligned16(galpha))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "galpha must be 16-byte aligned");
+  const size_t need = (size_t)(weight_part_floats(plan, n_rows, needed) +
+                               split_part_floats(plan, n_rows, needed)) * sizeof(float);
+  if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(O2MI_ERR_WORKSPACE,
+                "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
   if (needed & 7) {
+    Args b = a;
+    const int splits = stream_splits(plan, n_rows);
+    if (splits > 1 && (needed & 6)) {
+      // Split channels: dy / dhidden partials after the affine-adjoint ones.
+      float* part = static_cast<float*>(workspace) + weight_part_floats(plan, n_rows, needed);
+      if (needed & 2) {
+        b.part_dy = part;
+        part += (int64_t)splits * n_rows * plan->W2;
+      }
+      if (needed & 4) b.part_gh = part;
+    }
     O2miTimed timed;
     const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_RADIAL_BACKWARD);
-    const hipError_t err = plan->set->backward(a, grad_output, gx, gy, ghidden, needed & 7, s);
+    hipError_t err = plan->set->backward(b, grad_output, gx, gy, ghidden, needed & 7, s);
     if (timing) o2mi_timing_end(s, &timed);
     if (err != hipSuccess) return fail_hip(err, "radial backward launch");
+    if (b.part_dy)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n_rows * plan->W2)), dim3(256), 0, s,
+                         b.part_dy, splits, n_rows * plan->W2, gy);
+    if (b.part_gh)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n_rows * plan->H)), dim3(256), 0, s,
+                         b.part_gh, splits, n_rows * plan->H, ghidden);
+    err = hipGetLastError();
+    if (err != hipSuccess) return fail_hip(err, "radial split sum launch");
   }
   if (needed & 24) {
     int64_t per = 0;
     int slices = 0;
     slicing(plan, n_rows, &per, &slices);
-    const size_t need = (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
-    if (!workspace || workspace_bytes < need || !aligned16(workspace))
-      return fail(O2MI_ERR_WORKSPACE,
-                  "workspace smaller than o2mi_radial_backward_workspace_bytes or misaligned");
     float* part_alpha = static_cast<float*>(workspace);
     float* part_bias = part_alpha + (int64_t)slices * rows * plan->H;
     O2miTimed timed;
@@ -263,12 +322,9 @@ int o2mi_radial_forward_gather_f32(const o2mi_radial_plan* plan, const float* x_
 
 size_t o2mi_radial_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
                                             int needed) {
-  if (!plan || n_rows <= 0 || !(needed & 24)) return 0;
-  int64_t per = 0;
-  int slices = 0;
-  slicing(plan, n_rows, &per, &slices);
-  const int64_t rows = (int64_t)plan->set->paths * plan->C;
-  return (size_t)slices * (size_t)(rows * plan->H + rows) * sizeof(float);
+  if (!plan || n_rows <= 0 || (needed & ~31)) return 0;
+  return (size_t)(weight_part_floats(plan, n_rows, needed) +
+                  split_part_floats(plan, n_rows, needed)) * sizeof(float);
 }
 
 int o2mi_radial_backward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,

@@ -112,6 +112,13 @@ struct Args {
   // xindex[e]; an index outside [0, x_rows) reads zeros.
   const int64_t* xindex;
   int64_t x_rows;
+  // Streamed kernels: channels per block along grid y (a multiple of 16; C
+  // unless few edge blocks leave CUs idle).  Input adjoints split this way
+  // write per-split dy / dhidden partials (part_dy [splits][n][W2], part_gh
+  // [splits][n][H]) that a fixed-order sum finishes.
+  int tile_span;
+  float* part_dy;
+  float* part_gh;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int64_t row0,

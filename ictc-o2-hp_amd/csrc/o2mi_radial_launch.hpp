@@ -16,6 +16,7 @@ struct KernelSet {
   int kh;       // hidden width supported: <= 4 * kh
   int weight_edges;   // edges per staged tile of the affine-adjoint kernel
   int weight_groups;  // path groups (grid z) of the affine-adjoint kernel
+  int stream_edges;   // streamed kernels: edges per block (0: not streamed)
   hipError_t (*forward)(const Args&, float* out, hipStream_t);
   hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, float* ghid,
                          int needed, hipStream_t);
@@ -32,7 +33,8 @@ hipError_t launch_forward(const Args& a, float* out, hipStream_t s) {
   if constexpr (Plan::kStreamed)
     hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH>),
                        dim3((unsigned)((a.n + kEdgesPerWave * kSFwdWaves - 1) /
-                                       (kEdgesPerWave * kSFwdWaves))),
+                                       (kEdgesPerWave * kSFwdWaves)),
+                            (unsigned)((a.C + a.tile_span - 1) / a.tile_span)),
                        dim3(64 * kSFwdWaves), 0, s, a, out);
   else
     hipLaunchKernelGGL((radial_forward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads),
@@ -46,7 +48,8 @@ hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* g
   if constexpr (Plan::kStreamed) {
     hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH>),
                        dim3((unsigned)((a.n + kEdgesPerWave * kSBwdWaves - 1) /
-                                       (kEdgesPerWave * kSBwdWaves))),
+                                       (kEdgesPerWave * kSBwdWaves)),
+                            (unsigned)((a.C + a.tile_span - 1) / a.tile_span)),
                        dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, ghid, needed);
   } else
     hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)),
@@ -68,6 +71,8 @@ hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_sli
   return hipGetLastError();
 }
 
+static_assert(kSFwdWaves == kSBwdWaves, "streamed kernels share one edge blocking");
+
 template <class Plan>
 constexpr int weight_groups() {
   if constexpr (Plan::kStreamed) return wgt_groups<Plan>();
@@ -78,6 +83,7 @@ template <class Plan, int KH>
 const KernelSet* kernel_set() {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
                                 Plan::kWeightEdges, weight_groups<Plan>(),
+                                Plan::kStreamed ? kEdgesPerWave * kSFwdWaves : 0,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>};
   return &set;

@@ -167,11 +167,13 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
     yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
   });
 
+  const int u_begin = blockIdx.y * a.tile_span;
+  const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  chunk_fetch<Plan, KH, NT, false, 0>(pf, a, 0);
+  chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u_begin);
   chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   int parity = 0;  // LDS buffer of the current chunk
-  for (int u0 = 0; u0 < a.C; u0 += 16) {
+  for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
     const int u = u0 + 4 * g;
     float xv[4 * NC];
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
       if constexpr (c + 1 < NCH) {
         chunk_fetch<Plan, KH, NT, false, c + 1>(pf, a, u0);
       } else {
-        if (u0 + 16 < a.C) chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u0 + 16);
+        if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u0 + 16);
       }
       const int buf = L::kBuf0 + parity * L::kBufFloats;
       // Laundered per chunk so that neither addresses nor the uniform
@@ -225,7 +227,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         for (int i = 0; i < 4 * O.dim; ++i) asm volatile("" : "+v"(ov[i]));
         if constexpr (last) store_entry<O.dim>(ro, xrow, O.off * a.C, u, ov);
       });
-      if (c + 1 < NCH || u0 + 16 < a.C)
+      if (c + 1 < NCH || u0 + 16 < u_end)
         chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
       parity ^= 1;
       __syncthreads();
@@ -260,7 +262,11 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
   const bool need_y = (needed & 2) != 0;
   const auto rdx = rows_rsrc(gx, e0, a.W1, (needed & 1) ? rows : 0);
-  const auto rgh = rows_rsrc(ghid, e0, a.H, (needed & 4) ? rows : 0);
+  // dy / dhidden: this block's channel split only, as partials, when the
+  // channels are split over grid y.
+  float* dy_base = a.part_dy ? a.part_dy + (int64_t)blockIdx.y * a.n * a.W2 : gy;
+  const auto rgh = rows_rsrc(a.part_gh ? a.part_gh + (int64_t)blockIdx.y * a.n * a.H : ghid, e0,
+                             a.H, (needed & 4) ? rows : 0);
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
   float hid[KH];
@@ -274,11 +280,13 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   f4 gh[G::kTiles];
   static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) { gh[decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
 
+  const int u_begin = blockIdx.y * a.tile_span;
+  const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  chunk_fetch<Plan, KH, NT, true, 0>(pf, a, 0);
+  chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u_begin);
   chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   int parity = 0;
-  for (int u0 = 0; u0 < a.C; u0 += 16) {
+  for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
     const int u = u0 + 4 * g;
     float gv[4 * NC];
@@ -300,7 +308,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       if constexpr (c + 1 < NCH) {
         chunk_fetch<Plan, KH, NT, true, c + 1>(pf, a, u0);
       } else {
-        if (u0 + 16 < a.C) chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u0 + 16);
+        if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u0 + 16);
       }
       const int buf = L::kBuf0 + parity * L::kBufFloats;
       int coef_off = L::kCoef, bias_off = buf + L::kBias + 4 * g;
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
         if constexpr (last) store_entry<X.dim>(rdx, xrow, X.off * a.C, u, dxc);
         __builtin_amdgcn_sched_barrier(0);
       });
-      if (c + 1 < NCH || u0 + 16 < a.C)
+      if (c + 1 < NCH || u0 + 16 < u_end)
         chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
       parity ^= 1;
       __syncthreads();
@@ -385,7 +393,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       dyv[c] += __shfl_xor(dyv[c], 32);
     });
     if (g == 0 && j < rows) {
-      float* dst = gy + (e0 + j) * a.W2;
+      float* dst = dy_base + (e0 + j) * a.W2;
       static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
     }
   }

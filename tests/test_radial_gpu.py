@@ -125,6 +125,50 @@ def test_streamed_affine_adjoints_reproducible():
         assert torch.equal(a, b)
 
 
+def test_streamed_channel_split_matches_unsplit():
+    """Below one edge block per CU the streamed kernels split the channels
+    over grid y (dy / dhidden as fixed-order sums of split partials).  A run
+    of 33,024 edges (258 blocks: unsplit) must equal the two halves (129
+    blocks each: channels split in two) row by row, and the oracle on a row
+    subset."""
+    tp, linear, module, plan = _build(32, 6, "full", "canonical", 64, True, 23)
+    n = 33024
+    torch.manual_seed(23)
+    x = torch.randn(n, tp.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.randn(n, tp.input2_dimension, device="cuda", requires_grad=True)
+    h = torch.randn(n, 64, device="cuda", requires_grad=True)
+    g = torch.randn(n, tp.input1_dimension, device="cuda")
+    params = (x, y, h, linear.weight, linear.bias)
+    print("case streamed split n=33024 C=32", flush=True)
+    out = module(x, y, h)
+    whole = torch.autograd.grad(out, params, g)
+    half = n // 2
+    parts = []
+    for lo, hi in ((0, half), (half, n)):
+        xs, ys, hs = (t.detach()[lo:hi].clone().requires_grad_() for t in (x, y, h))
+        o = module(xs, ys, hs)
+        parts.append((o,) + torch.autograd.grad(o, (xs, ys, hs, linear.weight, linear.bias),
+                                                g[lo:hi]))
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), torch.cat([parts[0][0], parts[1][0]]))
+    assert torch.equal(whole[0], torch.cat([parts[0][1], parts[1][1]]))
+    for k in (1, 2):   # dy, dhidden: split partial sums, another summation order
+        cat = torch.cat([parts[0][k + 1], parts[1][k + 1]]).double().cpu().numpy()
+        assert normalized_error(whole[k].double().cpu().numpy(), cat) <= TOL
+    for k in (3, 4):   # dalpha, dbias: linear in the rows
+        both = (parts[0][k + 1] + parts[1][k + 1]).double().cpu().numpy()
+        assert normalized_error(both, whole[k].double().cpu().numpy()) <= TOL
+    rows = np.random.default_rng(23).choice(n, 48, replace=False)
+    alpha = linear.weight.detach().double().cpu().numpy()
+    b = linear.bias.detach().double().cpu().numpy()
+    xs, ys, hs, gs = (t.detach()[rows].double().cpu().numpy() for t in (x, y, h, g))
+    ref_out = U.radial_forward(plan, xs, ys, hs, alpha, b)
+    assert normalized_error(ref_out, out.detach()[rows].double().cpu().numpy()) <= TOL
+    ref = U.radial_backward(plan, xs, ys, hs, alpha, b, gs)
+    for r, a in zip(ref[:3], whole[:3]):
+        assert normalized_error(r, a[rows].double().cpu().numpy()) <= TOL
+
+
 COMPOSED = [
     (24, 2, "canonical", "canonical", 64, {}),      # C % 16 != 0
     (16, 2, "canonical", "canonical", 6, {}),       # H % 4 != 0
