@@ -86,7 +86,6 @@ bool aligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15
 // grid y (whole 16-channel tiles, no empty split).
 int stream_span(const o2mi_radial_plan* p, int64_t n) {
   const int per_block = p->set->stream_edges;
-  if (per_block == 0) return p->C;
   const int64_t blocks = std::max<int64_t>(1, (n + per_block - 1) / per_block);
   const int64_t cus = device_cus();
   const int tiles = p->C / 16;

@@ -11,19 +11,17 @@
 // A[l%16][l/16] and B[l/16][l%16]; D[4*(l/16) + r][l%16] is accumulator r of
 // lane l.  Below, g = lane/16 and j = lane%16.
 //
-// Forward / input adjoints (radial_forward_kernel, radial_backward_kernel).
-// A block of 8 waves owns 128 edges, 16 per wave, and walks the channels in
-// tiles of 16.  Per tile it stages alpha rows p*C + u0 .. +15 of every path
-// (hidden width padded with zeros to 4*KH) and the bias in LDS.  The weight
-// tile is computed as W^T[channel, edge]: A = alpha (lane: row j, h = KH*g+s),
-// B = hidden (lane: edge j, h = KH*g+s), so lane (g, j) ends up holding the
+// Forward / input adjoints: o2mi_radial_streamed.hpp.  The weight tile is
+// computed as W^T[channel, edge]: A = alpha (lane: row j, h = KH*g+s), B =
+// hidden (lane: edge j, h = KH*g+s), so lane (g, j) ends up holding the
 // weights of edge j for channels u0 + 4g + r, r = 0..3, and loads x, g and
 // writes out / dx for exactly those (edge, channel) pairs.  The hidden
 // adjoint, dh[e, h] = sum_{p,u} gw[e, p, u] alpha[p*C + u, h], reuses the
 // weight adjoint gw in that accumulator layout as the B operand (K index =
 // channel 4g + s at step s) against alpha read transposed from LDS.
 //
-// Affine-parameter adjoints (radial_weight_kernel).  dalpha = gw^T hidden and
+// Affine-parameter adjoints (radial_weight_kernel, for structures with few
+// paths; radial_weight_streamed_kernel otherwise).  dalpha = gw^T hidden and
 // dbias = sum_e gw are sums over all edges.  A block owns one channel tile and
 // a contiguous slice of edges; each wave owns the paths p = wave (mod 8) and
 // keeps their dalpha tiles in accumulators for the whole slice.  Per 32 edges
@@ -64,7 +62,6 @@ using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kEdgesPerWave = 16;
-constexpr int kEdgesPerBlock = kEdgesPerWave * kWaves;
 constexpr uint32_t kIdle = 0x80000000u;
 constexpr int kRsrcFlags = 0x00020000;
 
@@ -81,18 +78,6 @@ struct Geom {
   static constexpr int kRow = kHid + 4;    // LDS row stride of the alpha tile (floats)
   static constexpr int kTiles = kHid / 16; // 16-row tiles of the hidden / alpha adjoints
   static_assert(KH % 4 == 0, "KH must be a multiple of 4");
-};
-
-// LDS of the forward / input-adjoint kernels, one array: couplings and bias
-// first, so that their uniform or lane-base addresses reach every path with a
-// 16-bit immediate offset, then the alpha tile.
-template <int P, int KH>
-struct ALayout {
-  static constexpr int kCoef = 0;
-  static constexpr int kBias = P * 8;
-  static constexpr int kAlpha = P * 24;
-  static constexpr int kFloats = kAlpha + P * 16 * Geom<KH>::kRow;
-  static_assert(kAlpha % 4 == 0, "alpha tile must be 16-byte aligned");
 };
 
 struct Args {
@@ -161,28 +146,6 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Stage alpha rows p*C + u0 + r (r < 16) of every path, zero-padded to the
-// padded hidden width, and the matching bias entries.
-template <int P, int KH>
-__device__ __forceinline__ void stage_alpha(float* s_mem, const Args& a, int u0) {
-  using G = Geom<KH>;
-  using L = ALayout<P, KH>;
-  float* s_alpha = s_mem + L::kAlpha;
-  float* s_bias = s_mem + L::kBias;
-  constexpr int kVec = G::kHid / 4;
-  for (int idx = threadIdx.x; idx < P * 16 * kVec; idx += kThreads) {
-    const int q = idx % kVec;
-    const int pr = idx / kVec;  // p * 16 + r
-    const int p = pr >> 4, r = pr & 15;
-    f4 v = {0.f, 0.f, 0.f, 0.f};
-    if (4 * q < a.H)
-      v = *reinterpret_cast<const f4*>(a.alpha + (int64_t)(p * a.C + u0 + r) * a.H + 4 * q);
-    *reinterpret_cast<f4*>(s_alpha + pr * G::kRow + 4 * q) = v;
-  }
-  for (int idx = threadIdx.x; idx < P * 16; idx += kThreads)
-    s_bias[idx] = a.bias ? a.bias[(idx >> 4) * a.C + u0 + (idx & 15)] : 0.f;
-}
-
 // The 4 x dim values of one first-input entry for channels u .. u+3 of one row.
 template <int Dim>
 __device__ __forceinline__ void load_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int off_c,
@@ -235,9 +198,10 @@ __device__ __forceinline__ void load_hidden(__amdgpu_buffer_rsrc_t rh, int H, in
   });
 }
 
-// W^T tile of path p: bias + sum_h alpha[p*C + u0 + 4g + r, h] hidden[j, h].
-// bias_off = kBias + 4g and arow_off = kAlpha + j*kRow + KH*g are the lane's
-// base offsets (laundered once per channel tile by the caller).
+// W^T tile of the path staged in LDS slot p: bias + sum_h alpha[path*C + u0 +
+// 4g + r, h] hidden[j, h].  bias_off (the slot-0 bias + 4g) and arow_off (the
+// slot-0 alpha row j + KH*g) are the lane's base offsets, laundered by the
+// caller.
 template <int KH>
 __device__ __forceinline__ f4 weight_tile(const float* s_mem, int bias_off, int arow_off, int p,
                                           const float* hid) {
@@ -253,189 +217,6 @@ __device__ __forceinline__ f4 weight_tile(const float* s_mem, int bias_off, int 
     w = mfma(av.w, hid[4 * q + 3], w);
   });
   return w;
-}
-
-template <class Plan, int KH>
-__global__ __launch_bounds__(kThreads, 1) void radial_forward_kernel(Args a, float* out) {
-  using G = Geom<KH>;
-  constexpr int P = Plan::kPaths;
-  constexpr int NC = Plan::kComps1;
-  using L = ALayout<P, KH>;
-  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
-  float* s_coef = s_mem + L::kCoef;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-  const int g = lane >> 4, j = lane & 15;
-  const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
-  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
-  const auto rx = x_rsrc(a, e0, rows);
-  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
-  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
-  const auto ro = rows_rsrc(out, e0, a.W1, rows);
-  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (out)
-  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
-
-  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
-  float hid[KH];
-  load_hidden<KH>(rh, a.H, g, j, hid);
-  float yv[Plan::kComps2];
-  static_for<Plan::kComps2>([&](auto cc) {
-    constexpr int c = decltype(cc)::value;
-    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
-  });
-
-  for (int u0 = 0; u0 < a.C; u0 += 16) {
-    __syncthreads();
-    stage_alpha<P, KH>(s_mem, a, u0);
-    __syncthreads();
-    const int u = u0 + 4 * g;
-    // Laundered per tile so that neither addresses nor the uniform coupling
-    // reads are hoisted out of the channel loop into registers.
-    int coef_off = L::kCoef, bias_off = L::kBias + 4 * g;
-    int arow_off = L::kAlpha + j * G::kRow + KH * g;
-    asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off));
-    const float* cf_tile = s_mem + coef_off;
-    float xv[4 * NC];
-    load_row<Plan>(rx, xsrc, a.C, u, xv);
-    float ov[4 * NC];
-    static_for<4 * NC>([&](auto ic) { ov[decltype(ic)::value] = 0.f; });
-    static_for<P>([&](auto pc) {
-      constexpr int p = decltype(pc)::value;
-      constexpr RPath ps = Plan::paths[p];
-      constexpr REntry X = Plan::e1[ps.i];
-      constexpr REntry Y = Plan::e2[ps.j];
-      constexpr REntry O = Plan::e1[ps.k];
-      const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, p, hid);
-      static_for<8>([&](auto sc) {
-        constexpr int slot = decltype(sc)::value;
-        constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-        if constexpr ((ps.mask >> slot) & 1) {
-          const float cy = cf_tile[p * 8 + slot] * yv[Y.base + ib];
-          static_for<4>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;
-            ov[4 * O.base + r * O.dim + c] += cy * (xv[4 * X.base + r * X.dim + ia] * w[r]);
-          });
-        }
-      });
-      // No scheduling barrier between paths here: letting the compiler issue
-      // the next path's LDS reads and MFMAs early is 5% faster for the
-      // forward (the input-adjoint kernel below keeps its barrier: +10%
-      // without it, from register pressure).
-    });
-    store_row<Plan>(ro, xrow, a.C, u, ov);
-  }
-}
-
-// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here).
-template <class Plan, int KH>
-__global__ __launch_bounds__(kThreads, 1) void radial_backward_kernel(Args a, const float* gout,
-                                                                       float* gx, float* gy,
-                                                                       float* ghid, int needed) {
-  using G = Geom<KH>;
-  constexpr int P = Plan::kPaths;
-  constexpr int NC = Plan::kComps1;
-  constexpr int NY = Plan::kComps2;
-  using L = ALayout<P, KH>;
-  __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
-  float* s_coef = s_mem + L::kCoef;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-  const int g = lane >> 4, j = lane & 15;
-  const int64_t e0 = (int64_t)blockIdx.x * kEdgesPerBlock + wave * kEdgesPerWave;
-  const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
-  const auto rx = x_rsrc(a, e0, rows);
-  const auto rg = rows_rsrc(gout, e0, a.W1, rows);
-  const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
-  const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
-  const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (g, dx)
-  const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
-  // Every role is computed; a role that is not requested gets a zero-size
-  // store descriptor.  Branches on the roles cost more registers (the
-  // compiler duplicates the channel loop) than the rarely skipped work.
-  const bool need_y = (needed & 2) != 0;
-  const auto rdx = rows_rsrc(gx, e0, a.W1, (needed & 1) ? rows : 0);
-  const auto rgh = rows_rsrc(ghid, e0, a.H, (needed & 4) ? rows : 0);
-
-  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
-  float hid[KH];
-  load_hidden<KH>(rh, a.H, g, j, hid);
-  float yv[NY], dyv[NY];
-  static_for<NY>([&](auto cc) {
-    constexpr int c = decltype(cc)::value;
-    yv[c] = ld1(ry, (uint32_t)(j * a.W2 + c) * 4u);
-    dyv[c] = 0.f;
-  });
-  f4 gh[G::kTiles];
-  static_for<G::kTiles>([&](auto tc) { gh[decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
-
-  for (int u0 = 0; u0 < a.C; u0 += 16) {
-    __syncthreads();
-    stage_alpha<P, KH>(s_mem, a, u0);
-    __syncthreads();
-    const int u = u0 + 4 * g;
-    int coef_off = L::kCoef, bias_off = L::kBias + 4 * g;
-    int arow_off = L::kAlpha + j * G::kRow + KH * g, acol_off = L::kAlpha + 4 * g * G::kRow + j;
-    asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off));
-    const float* cf_tile = s_mem + coef_off;
-    float xv[4 * NC], gv[4 * NC], dxv[4 * NC];
-    load_row<Plan>(rx, xsrc, a.C, u, xv);
-    load_row<Plan>(rg, xrow, a.C, u, gv);
-    static_for<4 * NC>([&](auto ic) { dxv[decltype(ic)::value] = 0.f; });
-    static_for<P>([&](auto pc) {
-      constexpr int p = decltype(pc)::value;
-      constexpr RPath ps = Plan::paths[p];
-      constexpr REntry X = Plan::e1[ps.i];
-      constexpr REntry Y = Plan::e2[ps.j];
-      constexpr REntry O = Plan::e1[ps.k];
-      const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, p, hid);
-      float gw[4] = {0.f, 0.f, 0.f, 0.f};
-      static_for<8>([&](auto sc) {
-        constexpr int slot = decltype(sc)::value;
-        constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-        if constexpr ((ps.mask >> slot) & 1) {
-          const float cf = cf_tile[p * 8 + slot];
-          const float cy = cf * yv[Y.base + ib];
-          static_for<4>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;
-            const float xr = xv[4 * X.base + r * X.dim + ia];
-            const float gr = gv[4 * O.base + r * O.dim + c];
-            gw[r] += cy * (xr * gr);
-            dyv[Y.base + ib] += cf * (xr * gr) * w[r];
-            dxv[4 * X.base + r * X.dim + ia] += cy * (gr * w[r]);
-          });
-        }
-      });
-      const float* acol = s_mem + acol_off + p * 16 * G::kRow;
-      static_for<G::kTiles>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        gh[t] = mfma(acol[16 * t], gw[0], gh[t]);
-        gh[t] = mfma(acol[G::kRow + 16 * t], gw[1], gh[t]);
-        gh[t] = mfma(acol[2 * G::kRow + 16 * t], gw[2], gh[t]);
-        gh[t] = mfma(acol[3 * G::kRow + 16 * t], gw[3], gh[t]);
-      });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    store_row<Plan>(rdx, xrow, a.C, u, dxv);
-  }
-  if (need_y) {
-    // Lanes j, j+16, j+32, j+48 hold the channel partial sums of edge j.
-    static_for<NY>([&](auto cc) {
-      constexpr int c = decltype(cc)::value;
-      dyv[c] += __shfl_xor(dyv[c], 16);
-      dyv[c] += __shfl_xor(dyv[c], 32);
-    });
-    if (g == 0 && j < rows) {
-      float* dst = gy + (e0 + j) * a.W2;
-      static_for<NY>([&](auto cc) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
-    }
-  }
-  static_for<G::kTiles>([&](auto tc) {
-    constexpr int t = decltype(tc)::value;
-    const int h = 16 * t + 4 * g;
-    st4(rgh, gh[t], h < a.H ? (uint32_t)(j * a.H + h) * 4u : kIdle);
-  });
 }
 
 // Staged tile of the affine-adjoint kernel: Plan::kWeightEdges edges of x and g

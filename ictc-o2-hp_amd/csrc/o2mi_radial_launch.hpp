@@ -16,7 +16,7 @@ struct KernelSet {
   int kh;       // hidden width supported: <= 4 * kh
   int weight_edges;   // edges per staged tile of the affine-adjoint kernel
   int weight_groups;  // path groups (grid z) of the affine-adjoint kernel
-  int stream_edges;   // streamed kernels: edges per block (0: not streamed)
+  int stream_edges;   // edges per block of the forward / input-adjoint kernels
   hipError_t (*forward)(const Args&, float* out, hipStream_t);
   hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, float* ghid,
                          int needed, hipStream_t);
@@ -24,66 +24,55 @@ struct KernelSet {
                        float* part_alpha, float* part_bias, hipStream_t);
 };
 
-inline unsigned edge_blocks(int64_t n) {
-  return (unsigned)((n + kEdgesPerBlock - 1) / kEdgesPerBlock);
+static_assert(kSFwdWaves == kSBwdWaves, "forward and input adjoints share one edge blocking");
+constexpr int kStreamEdges = kEdgesPerWave * kSFwdWaves;
+
+// Grid: edge blocks x channel splits (Args::tile_span).
+inline dim3 stream_grid(const Args& a) {
+  return dim3((unsigned)((a.n + kStreamEdges - 1) / kStreamEdges),
+              (unsigned)((a.C + a.tile_span - 1) / a.tile_span));
 }
 
 template <class Plan, int KH>
 hipError_t launch_forward(const Args& a, float* out, hipStream_t s) {
-  if constexpr (Plan::kStreamed)
-    hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH>),
-                       dim3((unsigned)((a.n + kEdgesPerWave * kSFwdWaves - 1) /
-                                       (kEdgesPerWave * kSFwdWaves)),
-                            (unsigned)((a.C + a.tile_span - 1) / a.tile_span)),
-                       dim3(64 * kSFwdWaves), 0, s, a, out);
-  else
-    hipLaunchKernelGGL((radial_forward_kernel<Plan, KH>), dim3(edge_blocks(a.n)), dim3(kThreads),
-                       0, s, a, out);
+  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH>), stream_grid(a),
+                     dim3(64 * kSFwdWaves), 0, s, a, out);
   return hipGetLastError();
 }
 
 template <class Plan, int KH>
 hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* gy, float* ghid,
                            int needed, hipStream_t s) {
-  if constexpr (Plan::kStreamed) {
-    hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH>),
-                       dim3((unsigned)((a.n + kEdgesPerWave * kSBwdWaves - 1) /
-                                       (kEdgesPerWave * kSBwdWaves)),
-                            (unsigned)((a.C + a.tile_span - 1) / a.tile_span)),
-                       dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, ghid, needed);
-  } else
-    hipLaunchKernelGGL((radial_backward_kernel<Plan, KH>), dim3(edge_blocks(a.n)),
-                       dim3(kThreads), 0, s, a, gout, gx, gy, ghid, needed);
+  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH>), stream_grid(a),
+                     dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, ghid, needed);
   return hipGetLastError();
 }
 
 template <class Plan, int KH>
 hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_slice, int slices,
                          float* part_alpha, float* part_bias, hipStream_t s) {
-  if constexpr (Plan::kStreamed)
+  if constexpr (Plan::kWgtStreamed)
     hipLaunchKernelGGL((radial_weight_streamed_kernel<Plan, KH>),
                        dim3((unsigned)slices, (unsigned)(a.C / 16), wgt_groups<Plan>()),
                        dim3(64 * kSWgtWaves), 0, s, a, gout, edges_per_slice, part_alpha,
                        part_bias);
   else
-    hipLaunchKernelGGL((radial_weight_kernel<Plan, KH>), dim3((unsigned)slices, (unsigned)(a.C / 16)),
-                       dim3(kThreads), 0, s, a, gout, edges_per_slice, part_alpha, part_bias);
+    hipLaunchKernelGGL((radial_weight_kernel<Plan, KH>),
+                       dim3((unsigned)slices, (unsigned)(a.C / 16)), dim3(kThreads), 0, s, a,
+                       gout, edges_per_slice, part_alpha, part_bias);
   return hipGetLastError();
 }
 
-static_assert(kSFwdWaves == kSBwdWaves, "streamed kernels share one edge blocking");
-
 template <class Plan>
 constexpr int weight_groups() {
-  if constexpr (Plan::kStreamed) return wgt_groups<Plan>();
+  if constexpr (Plan::kWgtStreamed) return wgt_groups<Plan>();
   else return 1;
 }
 
 template <class Plan, int KH>
 const KernelSet* kernel_set() {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
-                                Plan::kWeightEdges, weight_groups<Plan>(),
-                                Plan::kStreamed ? kEdgesPerWave * kSFwdWaves : 0,
+                                Plan::kWeightEdges, weight_groups<Plan>(), kStreamEdges,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>};
   return &set;

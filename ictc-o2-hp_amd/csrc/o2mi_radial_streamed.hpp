@@ -1,9 +1,11 @@
-// Streamed radial kernels: structures whose alpha tile of every path does
-// not fit LDS (RadialUvuTensorProduct with m_max 6 and a full first input has
-// 254 paths: 254 x 16 channels x 64 hidden floats = 1 MiB per channel tile).
+// Forward and input-adjoint kernels of the fused radial affine + V=1 uvu
+// product (RadialUvuTensorProduct), and the affine-adjoint kernel for
+// structures with many paths.  Alpha is streamed through LDS: the reference's
+// m_max 6 full/canonical benchmark structure has 254 paths, 254 x 16 channels
+// x 64 hidden floats = 1 MiB per channel tile, far more than LDS holds.
 //
-// Same lane mapping and MFMA weight tiles as radial_forward_kernel /
-// radial_backward_kernel, with two changes:
+// A block of 8 waves owns 128 edges, 16 per wave, and walks the channels in
+// tiles of 16 (see o2mi_radial.hpp for the MFMA weight tile and lane layout):
 //  * alpha and bias are staged in chunks of Plan::kChunk paths, double
 //    buffered: the global loads of chunk c + 1 are in flight while chunk c is
 //    consumed, and land in the other LDS buffer before the chunk barrier.  The
@@ -12,7 +14,8 @@
 //    accumulators live) or by first-input entry (input adjoints: one x and one
 //    dx entry live, the next x entry loaded a group ahead), so the per-lane
 //    state is one full row (4 channels x components) plus one entry.
-// The affine-parameter adjoints use radial_weight_kernel with path groups.
+//  * with fewer edge blocks than CUs the channel tiles are split over grid y;
+//    the input adjoints then write dy / dhidden per split for a fixed-order sum.
 #pragma once
 
 #include "o2mi_radial.hpp"
@@ -404,26 +407,24 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   });
 }
 
-// Affine-parameter adjoints of a streamed structure (dalpha = gw^T hidden,
-// dbias = sum_e gw).  Same staged tiles as radial_weight_kernel, but each wave
-// owns 8 consecutive paths of Plan::wgt (grouped by second-input entry): its
-// dalpha tiles, 8 paths x 64 hidden x 16 channels, stay in registers, and per
-// step it reads from LDS only the operand components its paths use (about a
-// third of them).  8 waves of 8 paths: two waves per SIMD, 19% faster than 4
-// waves of 16 paths (one wave per SIMD, half the LDS reads per MFMA).
-#ifndef O2MI_SWGT_WAVES
-#define O2MI_SWGT_WAVES 8
-#endif
-#ifndef O2MI_SWGT_PATHS
-#define O2MI_SWGT_PATHS 8
-#endif
-constexpr int kSWgtWaves = O2MI_SWGT_WAVES;
-constexpr int kSWgtPaths = O2MI_SWGT_PATHS;         // paths per wave
-constexpr int kSWgtGroup = kSWgtWaves * kSWgtPaths;  // paths per block (grid z)
+// Affine-parameter adjoints of a structure with many paths (dalpha = gw^T
+// hidden, dbias = sum_e gw).  Same staged tiles as radial_weight_kernel, but
+// each wave owns Plan::kWgtPaths (up to 8) consecutive paths of Plan::wgt
+// (grouped by second-input entry): their dalpha tiles, 64 hidden x 16
+// channels each, stay in registers, and per step the wave reads from LDS only
+// the operand components its paths use (about a third at 254 paths).  8 waves
+// of 8 paths: two waves per SIMD, 19% faster than 4 waves of 16 paths (one
+// wave per SIMD, half the LDS reads per MFMA).
+constexpr int kSWgtWaves = 8;
+
+template <class Plan>
+constexpr int wgt_group_paths() {
+  return kSWgtWaves * Plan::kWgtPaths;  // paths per block (grid z)
+}
 
 template <class Plan>
 constexpr int wgt_groups() {
-  return (Plan::kPaths + kSWgtGroup - 1) / kSWgtGroup;
+  return (Plan::kPaths + wgt_group_paths<Plan>() - 1) / wgt_group_paths<Plan>();
 }
 
 // Whether a path at positions [q0, q0 + n) of Plan::wgt uses entry e as its
@@ -439,8 +440,8 @@ constexpr bool wgt_uses(int q0, int n, int e) {
 
 template <class Plan, int KH, int Q0, int NPW>
 __device__ __forceinline__ void wgt_step(const float* buf, const float* cf, int edge, int j,
-                                         f4 (&ga)[kSWgtPaths][Geom<KH>::kTiles],
-                                         float (&gb)[kSWgtPaths]) {
+                                         f4 (&ga)[Plan::kWgtPaths][Geom<KH>::kTiles],
+                                         float (&gb)[Plan::kWgtPaths]) {
   using G = Geom<KH>;
   using T = WTile<Plan, KH, 64 * kSWgtWaves>;
   const float* sx = buf;
@@ -516,9 +517,9 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
   const int tiles = end > begin ? (int)((end - begin + kWeightEdges - 1) / kWeightEdges) : 0;
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_coef[idx] = a.coef[idx];
-  f4 ga[kSWgtPaths][G::kTiles];
-  float gb[kSWgtPaths];
-  static_for<kSWgtPaths>([&](auto qc) __attribute__((always_inline)) {
+  f4 ga[Plan::kWgtPaths][G::kTiles];
+  float gb[Plan::kWgtPaths];
+  static_for<Plan::kWgtPaths>([&](auto qc) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value;
     gb[q] = 0.f;
     static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
@@ -548,8 +549,8 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
       const float* cf = s_coef + coef_off;
       static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
         constexpr int w = decltype(wc)::value;
-        constexpr int q0 = G0 * kSWgtGroup + w * kSWgtPaths;
-        constexpr int np = P - q0 < kSWgtPaths ? P - q0 : kSWgtPaths;
+        constexpr int q0 = G0 * wgt_group_paths<Plan>() + w * Plan::kWgtPaths;
+        constexpr int np = P - q0 < Plan::kWgtPaths ? P - q0 : Plan::kWgtPaths;
         if constexpr (np > 0)
           if (wave == w) wgt_step<Plan, KH, q0, np>(buf, cf, 4 * s + g, j, ga, gb);
       });
@@ -563,8 +564,8 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
   float* pb = part_bias + (int64_t)blockIdx.x * PC;
   static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
     constexpr int w = decltype(wc)::value;
-    constexpr int q0 = G0 * kSWgtGroup + w * kSWgtPaths;
-    constexpr int np = P - q0 < kSWgtPaths ? P - q0 : kSWgtPaths;
+    constexpr int q0 = G0 * wgt_group_paths<Plan>() + w * Plan::kWgtPaths;
+    constexpr int np = P - q0 < Plan::kWgtPaths ? P - q0 : Plan::kWgtPaths;
     if constexpr (np > 0) {
       if (wave == w) {
         static_for<np>([&](auto qc) __attribute__((always_inline)) {

@@ -92,15 +92,44 @@ def test_batch_shapes_on_cpu():
 
 
 def test_fused_structure_table():
-    """The fused kernels cover the structures whose alpha tile fits in LDS."""
+    """Every m_max <= 6 structure with equal angular orders has fused kernels;
+    the generated traversal orders are permutations grouped as the kernels
+    assume, and the double-buffered alpha chunks fit in LDS."""
     import build_native
     from ictc_o2_hp.uvu_o2 import ReferenceUvuTensorProduct
     names = {build_native._radial_name(*s) for s in build_native.RADIAL_STRUCTURES}
     assert "R4c4c" in names                      # configs[4]: C64, m4, canonical
+    assert "R6f6c" in names                      # the reference's radial benchmark
+    assert len(names) == 28
     for m, parity, m2, parity2 in build_native.RADIAL_STRUCTURES:
         tp = ReferenceUvuTensorProduct(16, 1, m, parity=parity, m_max_in2=m2,
                                        parity_in2=parity2, shared_weights=False)
-        assert 4 * len(tp.paths) * (24 + 16 * 68) <= 160 * 1024
+        lds = 4 * (8 * len(tp.paths) + 2 * build_native.RADIAL_CHUNK * 16 * (1 + 68))
+        assert lds <= 160 * 1024
+
+
+def test_generated_orders_group_paths(tmp_path):
+    """fwd groups paths by output entry and bwd by first-input entry (each group
+    contiguous, so one entry of accumulators is live); wgt is a permutation."""
+    import re
+    import build_native
+    build_native.generate_radial("R6f6c", tmp_path)
+    text = (tmp_path / "o2mi_radial_plans.h").read_text()
+    paths = [tuple(map(int, t)) for t in
+             re.findall(r"\{(\d+), (\d+), (\d+), \d+\}", text.split("paths[kPaths] = ")[1]
+                        .split(";")[0])]
+    orders = {k: list(map(int, re.search(k + r"\[kPaths\] = \{([^}]*)\}", text)
+                          .group(1).split(", "))) for k in ("fwd", "bwd", "wgt")}
+    assert len(paths) == 254
+    for key, role in (("fwd", 2), ("bwd", 0), ("wgt", 1)):
+        order = orders[key]
+        assert sorted(order) == list(range(254))
+        keys = [paths[p][role] for p in order]
+        seen, last = set(), None
+        for k in keys:                            # contiguous groups
+            assert k == last or k not in seen
+            seen.add(k)
+            last = k
 
 
 def test_library_exports_radial_symbols():
@@ -133,7 +162,10 @@ def test_radial_plan_create_validation():
     assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 0, 64, ctypes.byref(handle)) == 0
     assert lib.o2mi_radial_paths(handle) == 254
     assert lib.o2mi_radial_plan_destroy(handle) == 0
-    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 1, 64, ctypes.byref(handle)) == -2
+    assert lib.o2mi_radial_plan_create(64, 6, 1, 6, 1, 64, ctypes.byref(handle)) == 0
+    assert lib.o2mi_radial_paths(handle) == 508
+    assert lib.o2mi_radial_plan_destroy(handle) == 0
+    assert lib.o2mi_radial_plan_create(64, 7, 0, 7, 0, 64, ctypes.byref(handle)) == -2
     assert lib.o2mi_radial_plan_create(0, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_plan_create(64, 4, 2, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_backward_workspace_bytes(None, 10, 31) == 0

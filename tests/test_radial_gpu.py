@@ -1,7 +1,8 @@
 """GPU parity of RadialUvuTensorProduct against the fp64 radial oracle (gate 1e-5).
 
-Fused structures run the gfx950 radial kernels (weights generated on the
-matrix cores); the others run the composed GPU path (fp32 GEMM + uvu kernels).
+Fused structures (m_max <= 6, C % 16 == 0, H <= 64, H % 4 == 0) run the gfx950
+radial kernels (weights generated on the matrix cores); the others run the
+composed GPU path (fp32 GEMM + uvu kernels).
 """
 from __future__ import annotations
 
@@ -79,6 +80,11 @@ FUSED = [
     (48, 2, "canonical", "full", 64, {"normalization": "norm"}),
     (16, 3, "canonical", "canonical", 8, {"path_normalization": "element"}),
     (32, 0, "full", "full", 12, {}),
+    (16, 6, "canonical", "canonical", 64, {}),            # 64 paths
+    (32, 5, "full", "canonical", 32, {"normalization": "norm"}),
+    (16, 4, "canonical", "full", 40, {"path_normalization": "path"}),
+    (16, 3, "full", "full", 64, {}),                      # 148 paths
+    (16, 6, "full", "full", 16, {}),                      # 508 paths
 ]
 
 
@@ -172,7 +178,7 @@ def test_streamed_channel_split_matches_unsplit():
 COMPOSED = [
     (24, 2, "canonical", "canonical", 64, {}),      # C % 16 != 0
     (16, 2, "canonical", "canonical", 6, {}),       # H % 4 != 0
-    (16, 6, "full", "full", 64, {}),                # 508 paths: no kernel compiled
+    (16, 7, "canonical", "canonical", 64, {}),      # m_max 7: no kernel compiled
     (16, 2, "canonical", "canonical", 96, {}),      # H > 64
 ]
 
