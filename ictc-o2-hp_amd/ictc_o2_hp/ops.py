@@ -9,8 +9,8 @@ path_coefficients, metadata_id) -> (grad_left, grad_right, grad_weight)``.
 metadata, carried for schema compatibility (the compiled kernels embed the
 same table).  Each op has a fake implementation and autograd, so
 ``torch.compile(fullgraph=True)`` traces through it; the backward's own
-derivative (second order) recomputes with the PyTorch algebra, as the
-reference does (``triton_o2.py:1035-1069``).
+derivative (second order) is built from the same two ops by multilinearity
+(the reference differentiates its PyTorch algebra, ``triton_o2.py:1035-1069``).
 
 Outputs and workspaces come from torch's caching allocator; kernels run on
 the current stream.  A CUDA tensor without the built library raises.
@@ -26,7 +26,6 @@ import torch
 from . import __version__
 from . import _native
 from .plan import TPPlan
-from .torch_algebra import flat_forward
 
 NAMESPACE = "ictc_o2_hp_amd_v" + __version__.replace(".", "_")
 
@@ -156,27 +155,46 @@ o2_forward.register_autograd(_forward_backward, setup_context=_forward_setup)
 
 
 def _backward_setup(ctx, inputs, output):
-    left, right, weight, grad_output, _info, _coef, metadata_id = inputs
-    ctx.save_for_backward(left, right, weight, grad_output)
+    left, right, weight, grad_output, path_info, path_coefficients, metadata_id = inputs
+    ctx.save_for_backward(left, right, weight, grad_output, path_info, path_coefficients)
     ctx.metadata_id = metadata_id
+    ctx.set_materialize_grads(False)
 
 
 def _backward_backward(ctx, dd_left, dd_right, dd_weight):
-    """Second order: differentiate the first VJP of the PyTorch algebra."""
-    left, right, weight, grad_output = ctx.saved_tensors
-    selected = [(i, c) for i, c in enumerate((dd_left, dd_right, dd_weight)) if c is not None]
-    if not selected:
-        return (None,) * 7
-    entry = registered(ctx.metadata_id)
-    with torch.enable_grad():
-        inputs = tuple(t.detach().requires_grad_(True)
-                       for t in (left, right, weight, grad_output))
-        value = flat_forward(*inputs[:3], entry.plan, entry.layout)
-        first = torch.autograd.grad(value, inputs[:3], inputs[3], create_graph=True)
-        second = torch.autograd.grad(tuple(first[i] for i, _ in selected), inputs,
-                                     grad_outputs=tuple(c for _, c in selected),
-                                     allow_unused=True)
-    return (*second, None, None, None)
+    """Second order by multilinearity.  out = F(x, y, w) is linear in each of
+    x, y and w, and the first VJP is (F_x^T g, F_y^T g, F_w^T g), so
+
+        <dd_x, dx> + <dd_y, dy> + <dd_w, dw>
+            = <g, F(dd_x, y, w) + F(x, dd_y, w) + F(x, y, dd_w)>.
+
+    Each incoming cotangent is one first-order call with that operand
+    replaced: its VJP gives the gradients of the two other operands and its
+    value the gradient of g.  The calls are the kernel ops themselves, so
+    higher orders compose.  (The reference differentiates its PyTorch algebra
+    here, ``triton_o2.py:1041-1064``; the results agree to fp32 rounding.)"""
+    left, right, weight, grad_output, path_info, path_coefficients = ctx.saved_tensors
+    wanted = ctx.needs_input_grad[:4]
+    total = [None] * 4
+
+    def add(x, y, w, roles):
+        roles = [i for i in roles if wanted[i]]
+        if roles:
+            grads = o2_backward(x, y, w, grad_output, path_info, path_coefficients,
+                                ctx.metadata_id)
+            for i in roles:
+                total[i] = grads[i] if total[i] is None else total[i] + grads[i]
+        if wanted[3]:
+            value = o2_forward(x, y, w, path_info, path_coefficients, ctx.metadata_id)
+            total[3] = value if total[3] is None else total[3] + value
+
+    if dd_left is not None:
+        add(dd_left.contiguous(), right, weight, (1, 2))
+    if dd_right is not None:
+        add(left, dd_right.contiguous(), weight, (0, 2))
+    if dd_weight is not None:
+        add(left, right, dd_weight.contiguous(), (0, 1))
+    return (*total, None, None, None)
 
 
 o2_backward.register_autograd(_backward_backward, setup_context=_backward_setup)

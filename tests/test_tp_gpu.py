@@ -219,6 +219,42 @@ def test_double_backward_matches_fp64():
     assert O.normalized_error(hx64.numpy(), hx.double().cpu().numpy()) <= TOL
 
 
+def _orders_1_to_3(module, x, y):
+    """First VJP of a loss whose cotangent depends on the output, second order
+    with cotangents on all three first-order results, and third order."""
+    out = module(x, y)
+    e = (out * out.roll(1, 0)).sum()
+    gx, gy, gw = torch.autograd.grad(e, (x, y, module.weight), create_graph=True)
+    s = gx.square().sum() + (gy * y).sum() + gw.square().sum()
+    hx, hy, hw = torch.autograd.grad(s, (x, y, module.weight), create_graph=True)
+    t = hx.sum() + hy.square().sum() + (hw * hw.flip(0)).sum()
+    return (gx, gy, gw, hx, hy, hw) + torch.autograd.grad(t, (x, y, module.weight))
+
+
+@pytest.mark.parametrize("parity,layout", [("full", "tp"), ("canonical", "component")])
+def test_second_and_third_order_match_fp64(parity, layout):
+    """The second order is built from the kernel ops by multilinearity; the
+    orders above compose through the same ops."""
+    from ictc_o2_hp import ComponentMajorTensorProduct, TensorProduct
+    cls = TensorProduct if layout == "tp" else ComponentMajorTensorProduct
+    torch.manual_seed(7)
+    module = cls(8, 3, parity=parity).cuda()
+    with torch.no_grad():
+        module.weight.normal_()
+    x = torch.randn(37, module.representation_dimension, device="cuda", requires_grad=True)
+    y = torch.randn_like(x, requires_grad=True)
+    print(f"case orders 1-3 {cls.__name__} {parity}", flush=True)
+    got = _orders_1_to_3(module, x, y)
+    module64 = cls(8, 3, parity=parity).double()
+    module64.weight.data.copy_(module.weight.data.double().cpu())
+    module64.internal_compute_dtype = torch.float64
+    x64 = x.detach().double().cpu().requires_grad_()
+    y64 = y.detach().double().cpu().requires_grad_()
+    want = _orders_1_to_3(module64, x64, y64)
+    for name, r, a in zip(("gx", "gy", "gw", "hx", "hy", "hw", "tx", "ty", "tw"), want, got):
+        assert O.normalized_error(r.detach().numpy(), a.detach().double().cpu().numpy()) <= TOL, name
+
+
 def test_native_library_is_loaded():
     """The GPU path must run the in-tree HIP library (no silent fallback)."""
     from ictc_o2_hp import _native

@@ -158,3 +158,34 @@ def test_uvu_double_backward():
     (gy64,) = torch.autograd.grad(m64(x64, y64, w64).square().sum(), y64, create_graph=True)
     (hw64,) = torch.autograd.grad(gy64.sum(), w64)
     assert normalized_error(hw64.numpy(), hw.double().cpu().numpy()) <= TOL
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_uvu_second_and_third_order(shared):
+    """Cotangents on all three first-order results, the grad_output term, and
+    third order, against the fp64 CPU module."""
+    from ictc_o2_hp import UvuTensorProduct
+    torch.manual_seed(3)
+    module = UvuTensorProduct(8, 2, 2, parity="full", shared_weights=shared).cuda()
+    n = 21
+    x = torch.randn(n, module.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.randn(n, module.input2_dimension, device="cuda", requires_grad=True)
+    wshape = (module.weight_numel,) if shared else (n, module.weight_numel)
+    w = torch.randn(wshape, device="cuda", requires_grad=True)
+
+    def orders(mod, a, b, c):
+        out = mod(a, b, c)
+        e = (out * out.roll(1, 0)).sum()
+        ga, gb, gc = torch.autograd.grad(e, (a, b, c), create_graph=True)
+        s = ga.square().sum() + (gb * b).sum() + gc.square().sum()
+        ha, hb, hc = torch.autograd.grad(s, (a, b, c), create_graph=True)
+        t = ha.sum() + hb.square().sum() + hc.sum()
+        return (ga, gb, gc, ha, hb, hc) + torch.autograd.grad(t, (a, b, c))
+
+    print(f"case uvu orders 1-3 shared={shared}", flush=True)
+    got = orders(module, x, y, w)
+    m64 = UvuTensorProduct(8, 2, 2, parity="full", shared_weights=shared).double()
+    x64, y64, w64 = (t.detach().double().cpu().requires_grad_() for t in (x, y, w))
+    want = orders(m64, x64, y64, w64)
+    for r, a in zip(want, got):
+        assert normalized_error(r.detach().numpy(), a.detach().double().cpu().numpy()) <= TOL
