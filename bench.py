@@ -52,9 +52,10 @@ def _args():
     p.add_argument("--no-stream-ceiling", action="store_true",
                    help="skip the HBM streaming-ceiling probe (tp workload)")
     p.add_argument("--workload", default="tp",
-                   choices=("tp", "radial", "uvu", "grid", "radial-grid"),
+                   choices=("tp", "radial", "uvu", "grid", "radial-grid", "force"),
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
-                        "radial-grid: the reference's published radial-chain points")
+                        "radial-grid: the reference's published radial-chain points; "
+                        "force: a second-order (force-loss) step through the TP")
     p.add_argument("--grid-out", default=None, help="grid: also write the records to this file")
     p.add_argument("--radial-point", default=None,
                    help="radial-grid: only this 'edges,channels' point (e.g. 131072,64)")
@@ -354,6 +355,47 @@ def uvu_main(args):
     print(json.dumps(record), flush=True)
 
 
+def force_main(args):
+    """Force-loss step through TensorProduct (C, m_max, parity from the flags;
+    rows default 16,384): E = sum(out * out), F = dE/dx with create_graph,
+    then the gradients of sum(F^2) with respect to y and the weights, i.e. the
+    TP's second order.  Not a BASELINE metric: the reference computes this
+    order with its PyTorch algebra."""
+    import torch
+    from ictc_o2_hp import TensorProduct, _native
+
+    device = torch.device("cuda:0")
+    _native.library()
+    n = args.rows if args.rows != 131072 else 16384
+    torch.manual_seed(5)
+    module = TensorProduct(args.channels, args.m_max, parity=args.parity).to(device)
+    x = torch.randn(n, module.representation_dimension, device=device, requires_grad=True)
+    y = torch.randn_like(x, requires_grad=True)
+
+    def step():
+        out = module(x, y)
+        (forces,) = torch.autograd.grad((out * out).sum(), x, create_graph=True)
+        return torch.autograd.grad(forces.square().sum(), (y, module.weight))
+
+    torch.cuda.reset_peak_memory_stats(device)
+    ms_per_step, wall_ms, kinds, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    median, iqr = _sample_stats(samples)
+    record = {
+        "metric": "TP force-loss step rows/s (second order)", "value": n / (ms_per_step * 1e-3),
+        "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: x, y ~ N(0,1) (seeded), default-initialised weights",
+        "config": {"workload": f"TensorProduct C{args.channels} m{args.m_max} {args.parity} "
+                               f"N={n}: forces by create_graph, grads of sum(F^2) wrt y, w",
+                   "rows": n},
+        "ms_per_step_median": median, "ms_per_step_iqr": iqr, "wall_ms_per_step": wall_ms,
+        "kernel_launches": {k: kinds[k][1] for k in ("tp_forward", "tp_backward")},
+        "peak_allocated_MiB": torch.cuda.max_memory_allocated(device) / 2**20,
+    }
+    print(json.dumps(record), flush=True)
+
+
 # Published A100 times (ms) of the reference's TensorProduct, forward and
 # forward + full VJP, for every point of its benchmark matrix
 # (benchmarks/eqx/results/complete_matrix.csv, candidate_ms, 4 significant
@@ -647,6 +689,8 @@ def main():
         return grid_main(args)
     if args.workload == "radial-grid":
         return radial_grid_main(args)
+    if args.workload == "force":
+        return force_main(args)
     if args.workload != "tp":
         (radial_main if args.workload == "radial" else uvu_main)(args)
         return _copy_probe(args)
