@@ -276,10 +276,35 @@ __device__ __forceinline__ uint32_t tile_row_off(const Args& a, int64_t rows_of_
   return (id >= 0 && id < a.x_rows) ? (uint32_t)id * (uint32_t)a.W1 * 4u : kIdle;
 }
 
+// Byte offsets of this thread's x / g tile elements inside a tile's edge rows
+// (kIdle past the tile), and their column part: the same for every tile of a
+// block, so computed once (the entry lookup is a compare chain per element).
+template <class Plan, int KH, int NT = kThreads>
+struct WCols {
+  uint32_t voff[WTile<Plan, KH, NT>::kXPer], col[WTile<Plan, KH, NT>::kXPer];
+};
+
+template <class Plan, int KH, int NT = kThreads>
+__device__ __forceinline__ void weight_cols(WCols<Plan, KH, NT>& c, const Args& a, int u0) {
+  using T = WTile<Plan, KH, NT>;
+  constexpr int XE = 16 * Plan::kComps1;
+  static_for<T::kXPer>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = threadIdx.x + k * NT;
+    c.voff[k] = c.col[k] = kIdle;
+    if (idx < Plan::kWeightEdges * XE) {
+      const int edge = idx / XE;
+      c.col[k] = (uint32_t)tile_x_offset<Plan>(idx - edge * XE, a.C, u0) * 4u;
+      c.voff[k] = (uint32_t)(edge * a.W1) * 4u + c.col[k];
+    }
+  });
+}
+
 template <class Plan, int KH, int NT = kThreads>
 __device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH, NT>& pf, const Args& a,
                                              const float* gout, int64_t t0, int64_t t_end,
-                                             int u0, int64_t rows_of_tile) {
+                                             const WCols<Plan, KH, NT>& cols,
+                                             int64_t rows_of_tile) {
   using T = WTile<Plan, KH, NT>;
   constexpr int XE = 16 * Plan::kComps1;
   constexpr int kWeightEdges = Plan::kWeightEdges;
@@ -290,28 +315,22 @@ __device__ __forceinline__ void weight_fetch(WPrefetch<Plan, KH, NT>& pf, const 
   const auto rh = rows_rsrc(a.hidden, t0, a.H, rows);
   // Offsets first (the table rows come from other lanes), then every load, so
   // no load of the tile waits behind another.
-  uint32_t voff[T::kXPer], xoff[T::kXPer];
+  uint32_t xoff[T::kXPer];
   static_for<T::kXPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    const int idx = threadIdx.x + k * NT;
-    voff[k] = xoff[k] = kIdle;
-    if (idx < kWeightEdges * XE) {
-      const int edge = idx / XE;
-      const uint32_t col = (uint32_t)tile_x_offset<Plan>(idx - edge * XE, a.C, u0) * 4u;
-      voff[k] = (uint32_t)(edge * a.W1) * 4u + col;
-      if (a.xindex) {
-        const uint32_t row = edge < rows ? tile_row_off(a, rows_of_tile, edge) : kIdle;
-        xoff[k] = row == kIdle ? kIdle : row + col;
-      } else {
-        xoff[k] = voff[k];
-      }
+    xoff[k] = cols.voff[k];
+    if (a.xindex) {
+      const int edge = (threadIdx.x + k * NT) / XE;
+      const uint32_t row = (cols.col[k] != kIdle && edge < rows)
+                               ? tile_row_off(a, rows_of_tile, edge) : kIdle;
+      xoff[k] = row == kIdle ? kIdle : row + cols.col[k];
     }
   });
   __builtin_amdgcn_sched_barrier(0);
   static_for<T::kXPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     pf.x[k] = ld1(rx, xoff[k]);
-    pf.g[k] = ld1(rg, voff[k]);
+    pf.g[k] = ld1(rg, cols.voff[k]);
   });
   static_for<T::kYPer>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
@@ -392,9 +411,11 @@ __device__ __forceinline__ void weight_body(float* s_mem, const Args& a, const f
     static_for<G::kTiles>([&](auto tc) { ga[q][decltype(tc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
   });
 
+  WCols<Plan, KH> cols;
+  weight_cols<Plan, KH>(cols, a, u0);
   WPrefetch<Plan, KH> pf;
   if (tiles > 0) {
-    weight_fetch<Plan, KH>(pf, a, gout, begin, end, u0, tile_rows(a, begin, end));
+    weight_fetch<Plan, KH>(pf, a, gout, begin, end, cols, tile_rows(a, begin, end));
     weight_commit<Plan, KH>(pf, s_tile);
   }
   int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
@@ -403,7 +424,7 @@ __device__ __forceinline__ void weight_body(float* s_mem, const Args& a, const f
     const bool more = t + 1 < tiles;
     if (more) {
       const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
-      weight_fetch<Plan, KH>(pf, a, gout, t1, end, u0, next_rows);
+      weight_fetch<Plan, KH>(pf, a, gout, t1, end, cols, next_rows);
       next_rows = tile_rows(a, t1 + kWeightEdges, end);
     }
     const float* buf = s_tile + (t & 1) * T::kFloats;

@@ -527,9 +527,11 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
     });
   });
 
+  WCols<Plan, KH, NT> cols;
+  weight_cols<Plan, KH, NT>(cols, a, u0);
   WPrefetch<Plan, KH, NT> pf;
   if (tiles > 0) {
-    weight_fetch<Plan, KH, NT>(pf, a, gout, begin, end, u0, tile_rows(a, begin, end));
+    weight_fetch<Plan, KH, NT>(pf, a, gout, begin, end, cols, tile_rows(a, begin, end));
     weight_commit<Plan, KH, NT>(pf, s_tile);
   }
   int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
@@ -538,23 +540,27 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
     const bool more = t + 1 < tiles;
     if (more) {
       const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
-      weight_fetch<Plan, KH, NT>(pf, a, gout, t1, end, u0, next_rows);
+      weight_fetch<Plan, KH, NT>(pf, a, gout, t1, end, cols, next_rows);
       next_rows = tile_rows(a, t1 + kWeightEdges, end);
     }
     const float* buf = s_tile + (t & 1) * T::kFloats;
+    // One dispatch on the wave per tile (per step it cost 8% at configs[4]).
+    static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
+      constexpr int w = decltype(wc)::value;
+      constexpr int q0 = G0 * wgt_group_paths<Plan>() + w * Plan::kWgtPaths;
+      constexpr int np = P - q0 < Plan::kWgtPaths ? P - q0 : Plan::kWgtPaths;
+      if constexpr (np > 0) {
+        if (wave == w) {
 #pragma unroll
-    for (int s = 0; s < kWeightEdges / 4; ++s) {
-      int coef_off = 0;
-      asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
-      const float* cf = s_coef + coef_off;
-      static_for<kSWgtWaves>([&](auto wc) __attribute__((always_inline)) {
-        constexpr int w = decltype(wc)::value;
-        constexpr int q0 = G0 * wgt_group_paths<Plan>() + w * Plan::kWgtPaths;
-        constexpr int np = P - q0 < Plan::kWgtPaths ? P - q0 : Plan::kWgtPaths;
-        if constexpr (np > 0)
-          if (wave == w) wgt_step<Plan, KH, q0, np>(buf, cf, 4 * s + g, j, ga, gb);
-      });
-    }
+          for (int s = 0; s < kWeightEdges / 4; ++s) {
+            int coef_off = 0;
+            asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
+            const float* cf = s_coef + coef_off;
+            wgt_step<Plan, KH, q0, np>(buf, cf, 4 * s + g, j, ga, gb);
+          }
+        }
+      }
+    });
     if (more) weight_commit<Plan, KH, NT>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
     __syncthreads();
   }
