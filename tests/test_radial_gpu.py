@@ -116,6 +116,9 @@ def test_streamed_structure(c, hidden, n, bias, kw):
 @pytest.mark.parametrize("roles", [("x",), ("y",), ("hidden",), ("alpha",), ("y", "bias")])
 def test_streamed_gradient_roles(roles):
     _case(16, 6, "full", "canonical", 64, 70, seed=21, roles=roles)
+    # C = 48 with 70 edges: the channel tiles are split over grid y, so dy and
+    # dhidden come from the split partials (and are skipped when not requested).
+    _case(48, 6, "full", "canonical", 64, 70, seed=22, roles=roles)
 
 
 def test_streamed_affine_adjoints_reproducible():
@@ -199,6 +202,7 @@ def test_without_bias():
                                    ("x", "alpha"), ("hidden",)])
 def test_gradient_roles(roles):
     _case(16, 4, "canonical", "canonical", 64, 130, seed=11, roles=roles)
+    _case(64, 4, "canonical", "canonical", 64, 130, seed=12, roles=roles)   # split channels
 
 
 def test_empty_edges():
