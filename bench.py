@@ -52,7 +52,8 @@ def _args():
     p.add_argument("--no-stream-ceiling", action="store_true",
                    help="skip the HBM streaming-ceiling probe (tp workload)")
     p.add_argument("--workload", default="tp",
-                   choices=("tp", "radial", "uvu", "grid", "radial-grid", "force"),
+                   choices=("tp", "radial", "uvu", "uvu-shared", "grid", "radial-grid",
+                            "force"),
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
                         "radial-grid: the reference's published radial-chain points; "
                         "force: a second-order (force-loss) step through the TP")
@@ -351,6 +352,52 @@ def uvu_main(args):
                      "frac": bwd_gbs / HBM_PEAK_GBS if bwd_gbs else None,
                      "traffic": _traffic(REPO / "profiles" / "traffic.json",
                                          f"uvu_backward_C128_V32_m4_full_N{n}")},
+    }
+    print(json.dumps(record), flush=True)
+
+
+def uvu_shared_main(args):
+    """UvuTensorProduct in the reference's default mode (shared trainable
+    weights), V = 1: the example of its docs/UVU.md (C128, m6, full first
+    input, canonical second input, 16,384 rows), compiled, forward + gradients
+    of x, y and the weights with a ones cotangent.  Not a BASELINE metric."""
+    import torch
+    from ictc_o2_hp import UvuTensorProduct, _native
+
+    device = torch.device("cuda:0")
+    _native.library()
+    n = args.rows if args.rows != 131072 else 16384
+    torch.manual_seed(7)
+    module = UvuTensorProduct(128, 1, 6, parity="full", parity_in2="canonical").to(device)
+    x = torch.randn(n, module.input1_dimension, device=device, requires_grad=True)
+    y = torch.randn(n, module.input2_dimension, device=device, requires_grad=True)
+    cot = torch.ones_like(x)
+    run = module if args.no_compile else torch.compile(module, fullgraph=True, dynamic=False)
+
+    def step():
+        return torch.autograd.grad(run(x, y), (x, y, module.weight), cot)
+
+    ms_per_step, wall_ms, kinds, samples = _timed_steps(torch, step, args.steps, args.warmup)
+    median, iqr = _sample_stats(samples)
+    w1, w2 = module.input1_dimension, module.input2_dimension
+    per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in ("uvu_forward", "uvu_backward")}
+    alg_fwd, alg_bwd = 4.0 * n * (2 * w1 + w2), 4.0 * n * (3 * w1 + 2 * w2)
+    record = {
+        "metric": "uvu shared-weight V=1 fwd + VJP rows/s (docs/UVU.md example shape)",
+        "value": n / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: x, y ~ N(0,1) (seeded), default-initialised shared weights, "
+                "ones cotangent",
+        "config": {"workload": f"UvuTensorProduct C128 V1 m6 full/canonical shared weights "
+                               f"N={n} fwd+VJP (x, y, w)", "rows": n,
+                   "paths": module.weight_numel // 128},
+        "ms_per_step_median": median, "ms_per_step_iqr": iqr, "wall_ms_per_step": wall_ms,
+        "kernels_ms": {"forward": per["uvu_forward"], "backward": per["uvu_backward"]},
+        "kernels_GBps": {"forward": alg_fwd / (per["uvu_forward"] * 1e-3) / 1e9
+                         if per["uvu_forward"] else None,
+                         "backward": alg_bwd / (per["uvu_backward"] * 1e-3) / 1e9
+                         if per["uvu_backward"] else None},
     }
     print(json.dumps(record), flush=True)
 
@@ -691,6 +738,8 @@ def main():
         return radial_grid_main(args)
     if args.workload == "force":
         return force_main(args)
+    if args.workload == "uvu-shared":
+        return uvu_shared_main(args)
     if args.workload != "tp":
         (radial_main if args.workload == "radial" else uvu_main)(args)
         return _copy_probe(args)

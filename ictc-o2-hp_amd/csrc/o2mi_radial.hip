@@ -110,6 +110,19 @@ int64_t weight_part_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
   return (int64_t)slices * (rows * p->H + rows);
 }
 
+// Edge slices of the shared-weight gradient kernel: about one block (slice x
+// channel tile) per CU, whole staged tiles per slice.
+void dw_slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
+  const int64_t tiles_c = p->C / 16;
+  const int64_t want = std::max<int64_t>(1, (device_cus() + tiles_c - 1) / tiles_c);
+  const int64_t tile = p->set->dw_edges;
+  const int64_t edge_tiles = std::max<int64_t>(1, (n + tile - 1) / tile);
+  const int64_t s0 = std::min(want, edge_tiles);
+  const int64_t per = ((edge_tiles + s0 - 1) / s0) * tile;
+  *per_slice = per;
+  *slices = (int)std::max<int64_t>(1, (n + per - 1) / per);
+}
+
 int64_t split_part_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
   const int splits = stream_splits(p, n);
   if (splits <= 1 || n <= 0) return 0;
@@ -264,6 +277,16 @@ int radial_backward(const o2mi_radial_plan* plan, const Args& a, const float* gr
   return O2MI_OK;
 }
 
+// Shared-weight V = 1 uvu backward workspace: the dW slice partials, then the
+// split dy partials.
+int64_t shared_dw_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
+  if (!(needed & 4) || n <= 0) return 0;
+  int64_t per = 0;
+  int slices = 0;
+  dw_slicing(p, n, &per, &slices);
+  return (int64_t)slices * p->set->paths * p->C;
+}
+
 }  // namespace
 
 extern "C" {
@@ -350,6 +373,108 @@ int o2mi_radial_backward_gather_f32(const o2mi_radial_plan* plan, const float* x
   if (int st = gather_args(plan, &a, table_rows, index)) return st;
   return radial_backward(plan, a, grad_output, gx_edges, gy, ghidden, galpha, gbias, workspace,
                          workspace_bytes, needed, stream);
+}
+
+int o2mi_uvu_shared_plan_create(int channels, int m_max, int parity, int m_max_in2,
+                                int parity_in2, o2mi_radial_plan** plan) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  *plan = nullptr;
+  if (channels < 1 || m_max < 0 || m_max_in2 < 0 || (parity != 0 && parity != 1) ||
+      (parity_in2 != 0 && parity_in2 != 1))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid uvu plan arguments");
+  if (channels % 16 != 0)
+    return fail(O2MI_ERR_UNSUPPORTED, "shared-weight uvu kernels need channels % 16 == 0");
+  const KernelSet* set = o2mi_find_radial_set(m_max, parity, m_max_in2, parity_in2, 16);
+  if (!set)
+    return fail(O2MI_ERR_UNSUPPORTED, "no shared-weight uvu kernel compiled for this structure");
+  auto* p = new o2mi_radial_plan;
+  p->set = set;
+  p->C = channels;
+  p->H = 0;
+  p->W1 = (int64_t)channels * set->comps1;
+  p->W2 = set->comps2;
+  *plan = p;
+  return O2MI_OK;
+}
+
+int o2mi_uvu_shared_forward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                                const float* weight, const float* coefficients, float* out,
+                                int64_t n_rows, void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (n_rows == 0) return O2MI_OK;
+  if (!x || !y || !weight || !coefficients || !aligned16(x) || !aligned16(out))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input or misaligned x / out");
+  Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
+  const hipError_t err = plan->set->shared_forward(a, out, s);
+  if (timing) o2mi_timing_end(s, &timed);
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "shared uvu forward launch");
+}
+
+size_t o2mi_uvu_shared_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
+                                                int needed) {
+  if (!plan || n_rows <= 0 || (needed & ~7)) return 0;
+  return (size_t)(shared_dw_floats(plan, n_rows, needed) +
+                  split_part_floats(plan, n_rows, needed & 2)) * sizeof(float);
+}
+
+int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                                 const float* weight, const float* coefficients,
+                                 const float* grad_output, float* gx, float* gy, float* gweight,
+                                 void* workspace, size_t workspace_bytes, int64_t n_rows,
+                                 int needed, void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
+  if ((needed & 4) && !gweight)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL weight gradient for a requested role");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t wn = (int64_t)plan->set->paths * plan->C;
+  if (n_rows == 0) {
+    if (needed & 4)
+      hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(wn)), dim3(256), 0, s, gweight, wn);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? O2MI_OK : fail_hip(err, "shared uvu zero fill");
+  }
+  if (!x || !y || !weight || !coefficients || !aligned16(x))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input or misaligned x");
+  if (!grad_output || !aligned16(grad_output))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "grad_output must be a 16-byte aligned pointer");
+  if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
+  const int64_t dw_floats = shared_dw_floats(plan, n_rows, needed);
+  const size_t need = (size_t)(dw_floats + split_part_floats(plan, n_rows, needed & 2)) *
+                      sizeof(float);
+  if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(O2MI_ERR_WORKSPACE,
+                "workspace smaller than o2mi_uvu_shared_backward_workspace_bytes or misaligned");
+  Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);
+  if (needed & 3) {
+    const int splits = stream_splits(plan, n_rows);
+    if (splits > 1 && (needed & 2))
+      a.part_dy = static_cast<float*>(workspace) + dw_floats;
+    hipError_t err = plan->set->shared_backward(a, grad_output, gx, gy, needed & 3, s);
+    if (err != hipSuccess) return fail_hip(err, "shared uvu backward launch");
+    if (a.part_dy)
+      hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n_rows * plan->W2)), dim3(256), 0, s,
+                         a.part_dy, splits, n_rows * plan->W2, gy);
+  }
+  if (needed & 4) {
+    int64_t per = 0;
+    int slices = 0;
+    dw_slicing(plan, n_rows, &per, &slices);
+    float* part = static_cast<float*>(workspace);
+    hipError_t err = plan->set->shared_dw(a, grad_output, per, slices, part, s);
+    if (err != hipSuccess) return fail_hip(err, "shared uvu weight-gradient launch");
+    hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(wn)), dim3(256), 0, s, part, slices, wn,
+                       gweight);
+  }
+  if (timing) o2mi_timing_end(s, &timed);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "shared uvu launch");
 }
 
 }  // extern "C"

@@ -22,6 +22,13 @@ struct KernelSet {
                          int needed, hipStream_t);
   hipError_t (*weight)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
                        float* part_alpha, float* part_bias, hipStream_t);
+  // The V = 1 uvu product with shared weights (Args::alpha = weights [P][C]).
+  int dw_edges;       // edges per staged tile of the shared-weight gradient kernel
+  hipError_t (*shared_forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*shared_backward)(const Args&, const float* gout, float* gx, float* gy,
+                                int needed, hipStream_t);
+  hipError_t (*shared_dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
+                          float* part, hipStream_t);
 };
 
 static_assert(kSFwdWaves == kSBwdWaves, "forward and input adjoints share one edge blocking");
@@ -63,6 +70,30 @@ hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_sli
   return hipGetLastError();
 }
 
+template <class Plan, int KH>
+hipError_t launch_shared_forward(const Args& a, float* out, hipStream_t s) {
+  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, true>), stream_grid(a),
+                     dim3(64 * kSFwdWaves), 0, s, a, out);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+hipError_t launch_shared_backward(const Args& a, const float* gout, float* gx, float* gy,
+                                  int needed, hipStream_t s) {
+  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, true>), stream_grid(a),
+                     dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, nullptr, needed & 3);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+hipError_t launch_shared_dw(const Args& a, const float* gout, int64_t edges_per_slice,
+                            int slices, float* part, hipStream_t s) {
+  hipLaunchKernelGGL((uvu_shared_dw_kernel<Plan, KH>),
+                     dim3((unsigned)slices, (unsigned)(a.C / 16)), dim3(kThreads), 0, s, a, gout,
+                     edges_per_slice, part);
+  return hipGetLastError();
+}
+
 template <class Plan>
 constexpr int weight_groups() {
   if constexpr (Plan::kWgtStreamed) return wgt_groups<Plan>();
@@ -74,7 +105,9 @@ const KernelSet* kernel_set() {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
                                 Plan::kWeightEdges, weight_groups<Plan>(), kStreamEdges,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
-                                &launch_weight<Plan, KH>};
+                                &launch_weight<Plan, KH>, dw_edges<Plan, KH>(),
+                                &launch_shared_forward<Plan, KH>,
+                                &launch_shared_backward<Plan, KH>, &launch_shared_dw<Plan, KH>};
   return &set;
 }
 

@@ -44,6 +44,7 @@ struct SLayout {
   static constexpr int kFloats = kBuf0 + 2 * kBufFloats;
   static constexpr int kChunks = (Plan::kPaths + kChunk - 1) / kChunk;
   static_assert(kAlpha % 4 == 0 && kBufFloats % 4 == 0, "buffers must be 16-byte aligned");
+  static_assert(Plan::kPaths * 16 <= 2 * kBufFloats, "shared uvu weights fit the chunk buffers");
 };
 
 // Per-thread registers of one chunk in flight: alpha rows as float4 (hidden
@@ -130,6 +131,13 @@ constexpr bool entry_used(int e) {
   return false;
 }
 
+// Shared uvu weights W[p][u] (V = 1) of channel tile u0, all paths: [P][16].
+template <class Plan, int NT>
+__device__ __forceinline__ void stage_shared_weights(float* dst, const Args& a, int u0) {
+  for (int idx = threadIdx.x; idx < Plan::kPaths * 16; idx += NT)
+    dst[idx] = a.alpha[(idx >> 4) * a.C + u0 + (idx & 15)];
+}
+
 template <int Dim>
 __device__ __forceinline__ void store_zero_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off,
                                                  int off_c, int u) {
@@ -137,7 +145,10 @@ __device__ __forceinline__ void store_zero_entry(__amdgpu_buffer_rsrc_t r, uint3
   store_entry<Dim>(r, row_off, off_c, u, z);
 }
 
-template <class Plan, int KH>
+// kShared: the uvu product with shared weights (V = 1): a.alpha holds the
+// [P][C] weights, staged per channel tile instead of generated (no hidden, no
+// bias, no matrix cores).
+template <class Plan, int KH, bool kShared = false>
 __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_kernel(Args a,
                                                                                    float* out) {
   constexpr int NT = 64 * kSFwdWaves;
@@ -163,7 +174,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
   float hid[KH];
-  load_hidden<KH>(rh, a.H, g, j, hid);
+  if constexpr (!kShared) load_hidden<KH>(rh, a.H, g, j, hid);
   float yv[Plan::kComps2];
   static_for<Plan::kComps2>([&](auto cc) __attribute__((always_inline)) {
     constexpr int c = decltype(cc)::value;
@@ -173,11 +184,17 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   const int u_begin = blockIdx.y * a.tile_span;
   const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u_begin);
-  chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  if constexpr (!kShared) {
+    chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u_begin);
+    chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  }
   int parity = 0;  // LDS buffer of the current chunk
   for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
+    if constexpr (kShared) {
+      stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
+      __syncthreads();
+    }
     const int u = u0 + 4 * g;
     float xv[4 * NC];
     load_row<Plan>(rx, xsrc, a.C, u, xv);
@@ -189,17 +206,19 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
     float ov[8];
     static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
       constexpr int c = decltype(cc)::value;
-      if constexpr (c + 1 < NCH) {
-        chunk_fetch<Plan, KH, NT, false, c + 1>(pf, a, u0);
-      } else {
-        if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u0 + 16);
+      if constexpr (!kShared) {
+        if constexpr (c + 1 < NCH) {
+          chunk_fetch<Plan, KH, NT, false, c + 1>(pf, a, u0);
+        } else {
+          if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u0 + 16);
+        }
       }
       const int buf = L::kBuf0 + parity * L::kBufFloats;
       // Laundered per chunk so that neither addresses nor the uniform
       // coupling reads are hoisted into registers across chunks.
       int coef_off = L::kCoef, bias_off = buf + L::kBias + 4 * g;
-      int arow_off = buf + L::kAlpha + j * G::kRow + KH * g;
-      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off));
+      int arow_off = buf + L::kAlpha + j * G::kRow + KH * g, wsh_off = L::kBuf0 + 4 * g;
+      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(wsh_off));
       const float* cf = s_mem + coef_off;
       static_for<(P - c * PC < PC ? P - c * PC : PC)>([&](auto sc) __attribute__((always_inline)) {
         constexpr int slot = decltype(sc)::value;
@@ -212,7 +231,9 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         constexpr bool first = q == 0 || Plan::paths[Plan::fwd[q == 0 ? 0 : q - 1]].k != ps.k;
         constexpr bool last = q == P - 1 || Plan::paths[Plan::fwd[q == P - 1 ? q : q + 1]].k != ps.k;
         if constexpr (first) static_for<8>([&](auto ic) __attribute__((always_inline)) { ov[decltype(ic)::value] = 0.f; });
-        const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        f4 w;
+        if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
           constexpr int oc = sl >> 2, ia = (sl >> 1) & 1, ib = sl & 1;
@@ -230,16 +251,19 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         for (int i = 0; i < 4 * O.dim; ++i) asm volatile("" : "+v"(ov[i]));
         if constexpr (last) store_entry<O.dim>(ro, xrow, O.off * a.C, u, ov);
       });
-      if (c + 1 < NCH || u0 + 16 < u_end)
-        chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
-      parity ^= 1;
-      __syncthreads();
+      if constexpr (!kShared) {
+        if (c + 1 < NCH || u0 + 16 < u_end)
+          chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
+        parity ^= 1;
+        __syncthreads();
+      }
     });
   }
 }
 
-// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here).
-template <class Plan, int KH>
+// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here; kShared: as the
+// forward, no hidden adjoint).
+template <class Plan, int KH, bool kShared = false>
 __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_kernel(
     Args a, const float* gout, float* gx, float* gy, float* ghid, int needed) {
   constexpr int NT = 64 * kSBwdWaves;
@@ -273,7 +297,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
   float hid[KH];
-  load_hidden<KH>(rh, a.H, g, j, hid);
+  if constexpr (!kShared) load_hidden<KH>(rh, a.H, g, j, hid);
   float yv[NY], dyv[NY];
   static_for<NY>([&](auto cc) __attribute__((always_inline)) {
     constexpr int c = decltype(cc)::value;
@@ -286,11 +310,17 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   const int u_begin = blockIdx.y * a.tile_span;
   const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u_begin);
-  chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  if constexpr (!kShared) {
+    chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u_begin);
+    chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
+  }
   int parity = 0;
   for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
+    if constexpr (kShared) {
+      stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
+      __syncthreads();
+    }
     const int u = u0 + 4 * g;
     float gv[4 * NC];
     load_row<Plan>(rg, xrow, a.C, u, gv);
@@ -308,16 +338,19 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
     }
     static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
       constexpr int c = decltype(cc)::value;
-      if constexpr (c + 1 < NCH) {
-        chunk_fetch<Plan, KH, NT, true, c + 1>(pf, a, u0);
-      } else {
-        if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u0 + 16);
+      if constexpr (!kShared) {
+        if constexpr (c + 1 < NCH) {
+          chunk_fetch<Plan, KH, NT, true, c + 1>(pf, a, u0);
+        } else {
+          if (u0 + 16 < u_end) chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u0 + 16);
+        }
       }
       const int buf = L::kBuf0 + parity * L::kBufFloats;
       int coef_off = L::kCoef, bias_off = buf + L::kBias + 4 * g;
       int arow_off = buf + L::kAlpha + j * G::kRow + KH * g;
-      int acol_off = buf + L::kAlpha + 4 * g * G::kRow + j;
-      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off));
+      int acol_off = buf + L::kAlpha + 4 * g * G::kRow + j, wsh_off = L::kBuf0 + 4 * g;
+      asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(acol_off),
+                   "+v"(wsh_off));
       const float* cf = s_mem + coef_off;
       static_for<(P - c * PC < PC ? P - c * PC : PC)>([&](auto sc) __attribute__((always_inline)) {
         constexpr int slot = decltype(sc)::value;
@@ -347,7 +380,9 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
             }
           }
         }
-        const f4 w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        f4 w;
+        if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
         float gw[4] = {0.f, 0.f, 0.f, 0.f};
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
@@ -371,21 +406,25 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
         if constexpr (Y.dim == 2) asm volatile("" : "+v"(dyv[Y.base + 1]));
 #pragma unroll
         for (int i = 0; i < 4 * X.dim; ++i) asm volatile("" : "+v"(dxc[i]));
-        const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
-        static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
-          constexpr int t = decltype(tc)::value;
-          gh[t] = mfma(acol[16 * t], gw[0], gh[t]);
-          gh[t] = mfma(acol[G::kRow + 16 * t], gw[1], gh[t]);
-          gh[t] = mfma(acol[2 * G::kRow + 16 * t], gw[2], gh[t]);
-          gh[t] = mfma(acol[3 * G::kRow + 16 * t], gw[3], gh[t]);
-        });
+        if constexpr (!kShared) {
+          const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
+          static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+            constexpr int t = decltype(tc)::value;
+            gh[t] = mfma(acol[16 * t], gw[0], gh[t]);
+            gh[t] = mfma(acol[G::kRow + 16 * t], gw[1], gh[t]);
+            gh[t] = mfma(acol[2 * G::kRow + 16 * t], gw[2], gh[t]);
+            gh[t] = mfma(acol[3 * G::kRow + 16 * t], gw[3], gh[t]);
+          });
+        }
         if constexpr (last) store_entry<X.dim>(rdx, xrow, X.off * a.C, u, dxc);
         __builtin_amdgcn_sched_barrier(0);
       });
-      if (c + 1 < NCH || u0 + 16 < u_end)
-        chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
-      parity ^= 1;
-      __syncthreads();
+      if constexpr (!kShared) {
+        if (c + 1 < NCH || u0 + 16 < u_end)
+          chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
+        parity ^= 1;
+        __syncthreads();
+      }
     });
   }
   if (need_y) {
@@ -400,11 +439,12 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
     }
   }
-  static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
-    constexpr int t = decltype(tc)::value;
-    const int h = 16 * t + 4 * g;
-    st4(rgh, gh[t], h < a.H ? (uint32_t)(j * a.H + h) * 4u : kIdle);
-  });
+  if constexpr (!kShared)
+    static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value;
+      const int h = 16 * t + 4 * g;
+      st4(rgh, gh[t], h < a.H ? (uint32_t)(j * a.H + h) * 4u : kIdle);
+    });
 }
 
 // Affine-parameter adjoints of a structure with many paths (dalpha = gw^T

@@ -144,9 +144,9 @@ typedef struct o2mi_radial_plan o2mi_radial_plan;
 
 /* Plan for a uvu structure (m_max, parity, m_max_in2, parity_in2), C channels
  * and hidden width H.  O2MI_ERR_UNSUPPORTED when no fused kernel exists for
- * it (C % 16 != 0, H % 4 != 0, H > 64, or a structure whose alpha tile does
- * not fit in LDS); callers then compose the affine map and the uvu product.
- * Replaces the block policy of radial_streamed.py:17-34. */
+ * it (C % 16 != 0, H % 4 != 0, H > 64, m_max > 6 or m_max_in2 != m_max);
+ * callers then compose the affine map and the uvu product.  Replaces the
+ * block policy of radial_streamed.py:17-34. */
 int o2mi_radial_plan_create(int channels, int m_max, int parity, int m_max_in2,
                             int parity_in2, int hidden, o2mi_radial_plan **plan);
 int o2mi_radial_plan_destroy(o2mi_radial_plan *plan);
@@ -201,6 +201,36 @@ int o2mi_radial_backward_gather_f32(const o2mi_radial_plan *plan, const float *x
                                     float *dbias, void *workspace, size_t workspace_bytes,
                                     int64_t n_rows, int needed, void *stream);
 
+/* ---- V = 1 uvu product with shared weights ---------------------------------
+ * UvuTensorProduct(C, 1, m, parity=..., parity_in2=..., shared_weights=True),
+ * the reference's default weight mode: out[k, u] += sum over paths (i, j, k)
+ * of w[p, u] * CG_p(x[i, u], y[j]) (uvu_o2.py:50-73).  Layouts as the radial
+ * calls above, weights [P*C] in [path, channel] order.  Plans exist for the
+ * same structures as the radial plans (C % 16 == 0, m_max = m_max_in2 <= 6);
+ * destroy with o2mi_radial_plan_destroy. */
+int o2mi_uvu_shared_plan_create(int channels, int m_max, int parity, int m_max_in2,
+                                int parity_in2, o2mi_radial_plan **plan);
+
+/* out = uvu(x, y; w).  Replaces the uvu forward op for this mode
+ * (uvu_triton.py:235-284). */
+int o2mi_uvu_shared_forward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                                const float *weight, const float *coefficients, float *out,
+                                int64_t n_rows, void *stream);
+
+/* Workspace of o2mi_uvu_shared_backward_f32 (the weight gradient's edge-slice
+ * partials, and the dy partials when few rows split the channels). */
+size_t o2mi_uvu_shared_backward_workspace_bytes(const o2mi_radial_plan *plan, int64_t n_rows,
+                                                int needed);
+
+/* (gx, gy, gweight) for the roles in `needed` (1 x, 2 y, 4 weight): the uvu
+ * backward op for this mode (uvu_triton.py:287-414).  gweight [P*C] is a
+ * fixed-order fp32 sum over rows (zero for n_rows == 0). */
+int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                                 const float *weight, const float *coefficients,
+                                 const float *grad_output, float *gx, float *gy, float *gweight,
+                                 void *workspace, size_t workspace_bytes, int64_t n_rows,
+                                 int needed, void *stream);
+
 /* ---- row gather and deterministic row segment sums -------------------------
  * The node <-> edge data movement of a message-passing layer around the
  * radial product.  No counterpart in the reference, which gathers with
@@ -232,7 +262,8 @@ int o2mi_kernel_timing_read(double *forward_ms, int *forward_count, double *back
                             int *backward_count);
 /* Same, per kind: 0 TP forward, 1 TP backward, 2 radial forward, 3 radial
  * input adjoints (dx, dy, dhidden), 4 radial affine adjoints (dalpha, dbias),
- * 5 uvu per-row-weight forward, 6 uvu per-row-weight backward.
+ * 5 uvu forward (per-row-weight and shared-weight V = 1 kernels), 6 uvu
+ * backward (the same).
  * ms[k] and counts[k] for k < n_kinds. */
 int o2mi_kernel_timing_read_kinds(double *ms, int *counts, int n_kinds);
 

@@ -66,6 +66,44 @@ def test_uvu_parity(c, v, m, kw, shared, n):
     _case(c, v, m, kw, shared, n, seed=c * 100 + v * 10 + m)
 
 
+# V = 1 with shared weights (the reference's default mode) and m_max_in2 ==
+# m_max: the plan-specialised kernels shared with the radial product.
+SHARED_V1 = [
+    (16, 2, {"parity": "canonical"}, 300),
+    (128, 4, {"parity": "full"}, 129),                                    # channels split
+    (32, 6, {"parity": "full", "parity_in2": "canonical"}, 1000),
+    (48, 3, {"parity": "canonical", "parity_in2": "full", "path_normalization": "path"}, 70),
+    (16, 1, {"parity": "full", "normalization": "norm"}, 1),
+    (64, 6, {"parity": "full"}, 40),                                      # 508 paths
+]
+
+
+@pytest.mark.parametrize("c,m,kw,n", SHARED_V1)
+def test_uvu_shared_v1_kernels(c, m, kw, n):
+    from ictc_o2_hp import UvuTensorProduct, uvu_ops
+    _case(c, 1, m, kw, True, n, seed=c + m + n)
+    module = UvuTensorProduct(c, 1, m, shared_weights=True, **kw)
+    assert uvu_ops.shared_plan(module._kernel_metadata_id) is not None
+
+
+def test_uvu_shared_v1_roles_and_reproducible():
+    from ictc_o2_hp import UvuTensorProduct
+    for wrt in ((True, False, False), (False, True, False), (False, False, True),
+                (False, True, True)):
+        _case(64, 1, 4, {"parity": "full"}, True, 90, seed=8, wrt=wrt)
+    torch.manual_seed(9)
+    module = UvuTensorProduct(32, 1, 5, parity="full", parity_in2="canonical").cuda()
+    x = torch.randn(40000, module.input1_dimension, device="cuda")
+    y = torch.randn(40000, module.input2_dimension, device="cuda")
+    g = torch.randn_like(x)
+    first = torch.autograd.grad(module(x, y), module.weight, g)[0]
+    second = torch.autograd.grad(module(x, y), module.weight, g)[0]
+    assert torch.equal(first, second)
+    halves = sum(torch.autograd.grad(module(x[s:s + 20000], y[s:s + 20000]), module.weight,
+                                     g[s:s + 20000])[0] for s in (0, 20000))
+    assert normalized_error(first.double().cpu().numpy(), halves.double().cpu().numpy()) <= TOL
+
+
 @pytest.mark.parametrize("wrt", [(True, False, False), (False, True, False), (False, False, True),
                                  (True, False, True)])
 def test_uvu_gradient_roles(wrt):
