@@ -146,6 +146,37 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+#ifndef O2MI_COEF_VEC
+#define O2MI_COEF_VEC 1
+#endif
+
+// The couplings of path p from the [P][8] LDS table: with O2MI_COEF_VEC the
+// halves the path uses as 16-byte reads (one LDS instruction per half, not
+// one per slot), else one read per used slot.
+template <int Mask>
+struct PathCoefs {
+  f4 lo, hi;
+  const float* row;
+};
+
+template <int Mask>
+__device__ __forceinline__ PathCoefs<Mask> load_coefs(const float* cf, int p) {
+  PathCoefs<Mask> c;
+  c.row = cf + p * 8;
+  if constexpr (O2MI_COEF_VEC) {
+    if constexpr ((Mask & 0x0F) != 0) c.lo = *reinterpret_cast<const f4*>(c.row);
+    if constexpr ((Mask & 0xF0) != 0) c.hi = *reinterpret_cast<const f4*>(c.row + 4);
+  }
+  return c;
+}
+
+template <int Slot, int Mask>
+__device__ __forceinline__ float coef_at(const PathCoefs<Mask>& c) {
+  if constexpr (!O2MI_COEF_VEC) return c.row[Slot];
+  else if constexpr (Slot < 4) return c.lo[Slot];
+  else return c.hi[Slot - 4];
+}
+
 // The 4 x dim values of one first-input entry for channels u .. u+3 of one row.
 template <int Dim>
 __device__ __forceinline__ void load_entry(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int off_c,
@@ -466,6 +497,8 @@ __device__ __forceinline__ void weight_body(float* s_mem, const Args& a, const f
           constexpr REntry Y = Plan::e2[ps.j];
           constexpr REntry O = Plan::e1[ps.k];
           float gw = 0.f;
+          // Scalar coupling reads here: the 16-byte form measured slower in
+          // this resident kernel (more live registers across the path loop).
           static_for<8>([&](auto sc) {
             constexpr int slot = decltype(sc)::value;
             constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
@@ -521,110 +554,6 @@ constexpr int dw_edges() {
     return 16;
   else
     return 8;
-}
-
-// Shared-weight gradient of the V = 1 uvu product over one edge slice and one
-// channel tile: part[slice][p*C + u] = sum_e sum_slots coef y x g, the same
-// per-(edge, channel) weight adjoint as radial_weight_kernel forms, summed on
-// the VALU (one accumulator per path and lane: paths p = wave mod 8), then
-// over the lane's 4 edge rows by shuffles.  Grid (slices, C/16); the slice
-// partials are summed in a fixed order afterwards.
-template <class Plan, int KH>
-__global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, const float* gout,
-                                                                    int64_t edges_per_slice,
-                                                                    float* part) {
-  using TP = WithEdges<Plan, dw_edges<Plan, KH>()>;
-  using T = WTile<TP, KH>;
-  constexpr int P = Plan::kPaths;
-  constexpr int kE = TP::kWeightEdges;
-  constexpr int NPW = (P + kWaves - 1) / kWaves;
-  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
-  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
-  float* s_coef = s_mem;
-  float* s_tile = s_mem + kCoefPad;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-  const int g = lane >> 4, j = lane & 15;
-  const int u0 = blockIdx.y * 16;
-  const int64_t begin = (int64_t)blockIdx.x * edges_per_slice;
-  const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
-  const int tiles = end > begin ? (int)((end - begin + kE - 1) / kE) : 0;
-
-  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
-  float acc[NPW];
-  static_for<NPW>([&](auto qc) { acc[decltype(qc)::value] = 0.f; });
-
-  WCols<TP, KH> cols;
-  weight_cols<TP, KH>(cols, a, u0);
-  WPrefetch<TP, KH> pf;
-  if (tiles > 0) {
-    weight_fetch<TP, KH>(pf, a, gout, begin, end, cols, tile_rows(a, begin, end));
-    weight_commit<TP, KH>(pf, s_tile);
-  }
-  int64_t next_rows = tile_rows(a, begin + kE, end);
-  __syncthreads();
-  for (int t = 0; t < tiles; ++t) {
-    const bool more = t + 1 < tiles;
-    if (more) {
-      const int64_t t1 = begin + (int64_t)(t + 1) * kE;
-      weight_fetch<TP, KH>(pf, a, gout, t1, end, cols, next_rows);
-      next_rows = tile_rows(a, t1 + kE, end);
-    }
-    const float* buf = s_tile + (t & 1) * T::kFloats;
-    const float* sx = buf;
-    const float* sg = buf + T::kX;
-    const float* sy = buf + 2 * T::kX;
-#pragma unroll 2
-    for (int s = 0; s < kE / 4; ++s) {
-      const int edge = 4 * s + g;
-      int coef_off = 0;
-      asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
-      const float* cf_step = s_coef + coef_off;
-      float xv[Plan::kComps1], gv[Plan::kComps1], yv[Plan::kComps2];
-      static_for<Plan::kEntries1>([&](auto ec) {
-        constexpr REntry e = Plan::e1[decltype(ec)::value];
-        static_for<e.dim>([&](auto dc) {
-          constexpr int d = decltype(dc)::value;
-          const int o = edge * T::kXS + 16 * e.base + j * e.dim + d;
-          xv[e.base + d] = sx[o];
-          gv[e.base + d] = sg[o];
-        });
-      });
-      static_for<Plan::kComps2>([&](auto cc) {
-        yv[decltype(cc)::value] = sy[edge * T::kYS + decltype(cc)::value];
-      });
-      static_for<P>([&](auto pc) {
-        constexpr int p = decltype(pc)::value;
-        if (wave == p % kWaves) {
-          constexpr RPath ps = Plan::paths[p];
-          constexpr REntry X = Plan::e1[ps.i];
-          constexpr REntry Y = Plan::e2[ps.j];
-          constexpr REntry O = Plan::e1[ps.k];
-          static_for<8>([&](auto sc) {
-            constexpr int slot = decltype(sc)::value;
-            constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-            if constexpr ((ps.mask >> slot) & 1)
-              acc[p / kWaves] += cf_step[p * 8 + slot] * yv[Y.base + ib] *
-                                 (xv[X.base + ia] * gv[O.base + c]);
-          });
-        }
-      });
-    }
-    if (more) weight_commit<TP, KH>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
-    __syncthreads();
-  }
-
-  float* dst = part + (int64_t)blockIdx.x * P * a.C;
-  static_for<P>([&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    if (wave == p % kWaves) {
-      float v = acc[p / kWaves];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (g == 0) dst[(int64_t)p * a.C + u0 + j] = v;
-    }
-  });
 }
 
 // Grid (slices, C/16).  part_alpha: [slices][P*C][H]; part_bias: [slices][P*C].

@@ -100,21 +100,46 @@ constexpr int weight_groups() {
   else return 1;
 }
 
+// The shared-weight uvu launchers of a plan live in a translation unit of
+// their own (O2MI_DEFINE_UVU_SHARED): both halves of a large structure then
+// compile in parallel.
+struct SharedLaunchers {
+  hipError_t (*forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, int needed,
+                         hipStream_t);
+  hipError_t (*dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
+                   float* part, hipStream_t);
+};
+
 template <class Plan, int KH>
-const KernelSet* kernel_set() {
+const SharedLaunchers* shared_launchers() {
+  static const SharedLaunchers l = {&launch_shared_forward<Plan, KH>,
+                                    &launch_shared_backward<Plan, KH>,
+                                    &launch_shared_dw<Plan, KH>};
+  return &l;
+}
+
+template <class Plan, int KH>
+const KernelSet* kernel_set(const SharedLaunchers* shared) {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
                                 Plan::kWeightEdges, weight_groups<Plan>(), kStreamEdges,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>, dw_edges<Plan, KH>(),
-                                &launch_shared_forward<Plan, KH>,
-                                &launch_shared_backward<Plan, KH>, &launch_shared_dw<Plan, KH>};
+                                shared->forward, shared->backward, shared->dw};
   return &set;
 }
 
 }  // namespace radial
 }  // namespace o2mi
 
-#define O2MI_DEFINE_RADIAL_SET(NAME, KH)                                     \
-  const o2mi::radial::KernelSet* o2mi_radial_set_##NAME##_##KH() {           \
-    return o2mi::radial::kernel_set<o2mi::radial::plans::NAME, KH>();        \
+#define O2MI_DEFINE_RADIAL_SET(NAME, KH)                                                \
+  const o2mi::radial::SharedLaunchers* o2mi_uvu_shared_##NAME##_##KH();                  \
+  const o2mi::radial::KernelSet* o2mi_radial_set_##NAME##_##KH() {                      \
+    return o2mi::radial::kernel_set<o2mi::radial::plans::NAME, KH>(                     \
+        o2mi_uvu_shared_##NAME##_##KH());                                               \
+  }
+
+#define O2MI_DEFINE_UVU_SHARED(NAME, KH)                                                \
+  const o2mi::radial::SharedLaunchers* o2mi_uvu_shared_##NAME##_##KH() {                \
+    return o2mi::radial::shared_launchers<o2mi::radial::plans::NAME, KH>();              \
   }

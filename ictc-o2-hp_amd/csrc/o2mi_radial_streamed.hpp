@@ -234,11 +234,12 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         f4 w;
         if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
         else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        const auto cfs = load_coefs<ps.mask>(cf, p);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
           constexpr int oc = sl >> 2, ia = (sl >> 1) & 1, ib = sl & 1;
           if constexpr ((ps.mask >> sl) & 1) {
-            const float cy = cf[p * 8 + sl] * yv[Y.base + ib];
+            const float cy = coef_at<sl>(cfs) * yv[Y.base + ib];
             static_for<4>([&](auto rc) __attribute__((always_inline)) {
               constexpr int r = decltype(rc)::value;
               ov[r * O.dim + oc] += cy * (xv[4 * X.base + r * X.dim + ia] * w[r]);
@@ -384,11 +385,12 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
         if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
         else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
         float gw[4] = {0.f, 0.f, 0.f, 0.f};
+        const auto cfs = load_coefs<ps.mask>(cf, p);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
           constexpr int oc = sl >> 2, ia = (sl >> 1) & 1, ib = sl & 1;
           if constexpr ((ps.mask >> sl) & 1) {
-            const float cfv = cf[p * 8 + sl];
+            const float cfv = coef_at<sl>(cfs);
             const float cy = cfv * yv[Y.base + ib];
             static_for<4>([&](auto rc) __attribute__((always_inline)) {
               constexpr int r = decltype(rc)::value;
@@ -521,11 +523,12 @@ __device__ __forceinline__ void wgt_step(const float* buf, const float* cf, int 
     constexpr REntry Y = Plan::e2[ps.j];
     constexpr REntry O = Plan::e1[ps.k];
     float gw = 0.f;
+    const auto cfs = load_coefs<ps.mask>(cf, p);
     static_for<8>([&](auto sc) __attribute__((always_inline)) {
       constexpr int slot = decltype(sc)::value;
       constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
       if constexpr ((ps.mask >> slot) & 1)
-        gw += cf[p * 8 + slot] * yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+        gw += coef_at<slot>(cfs) * yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
     });
     gb[q] += gw;
     static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
@@ -626,6 +629,137 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
           b += __shfl_xor(b, 16);
           b += __shfl_xor(b, 32);
           if (g == 0) pb[row] = b;
+        });
+      }
+    }
+  });
+}
+
+// Shared-weight gradient of the V = 1 uvu product over one edge slice and one
+// channel tile: part[slice][p*C + u] = sum_e sum_slots coef y x g, the same
+// per-(edge, channel) weight adjoint as the affine-adjoint kernels form,
+// summed on the VALU.  Wave w owns ceil(P/8) consecutive paths of Plan::wgt
+// (one accumulator per path and lane) and reads from LDS only the operand
+// components they use; the dispatch on the wave is once per staged tile.  The
+// lane's 4 edge rows are summed by shuffles at the end.  Grid (slices, C/16);
+// the slice partials are summed in a fixed order afterwards.
+template <class Plan, int KH>
+__global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, const float* gout,
+                                                                    int64_t edges_per_slice,
+                                                                    float* part) {
+  using TP = WithEdges<Plan, dw_edges<Plan, KH>()>;
+  using T = WTile<TP, KH>;
+  constexpr int P = Plan::kPaths;
+  constexpr int kE = TP::kWeightEdges;
+  constexpr int NPW = (P + kWaves - 1) / kWaves;
+  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
+  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
+  float* s_coef = s_mem;
+  float* s_tile = s_mem + kCoefPad;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, j = lane & 15;
+  const int u0 = blockIdx.y * 16;
+  const int64_t begin = (int64_t)blockIdx.x * edges_per_slice;
+  const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
+  const int tiles = end > begin ? (int)((end - begin + kE - 1) / kE) : 0;
+
+  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
+  float acc[NPW];
+  static_for<NPW>([&](auto qc) __attribute__((always_inline)) { acc[decltype(qc)::value] = 0.f; });
+
+  WCols<TP, KH> cols;
+  weight_cols<TP, KH>(cols, a, u0);
+  WPrefetch<TP, KH> pf;
+  if (tiles > 0) {
+    weight_fetch<TP, KH>(pf, a, gout, begin, end, cols, tile_rows(a, begin, end));
+    weight_commit<TP, KH>(pf, s_tile);
+  }
+  int64_t next_rows = tile_rows(a, begin + kE, end);
+  __syncthreads();
+  for (int t = 0; t < tiles; ++t) {
+    const bool more = t + 1 < tiles;
+    if (more) {
+      const int64_t t1 = begin + (int64_t)(t + 1) * kE;
+      weight_fetch<TP, KH>(pf, a, gout, t1, end, cols, next_rows);
+      next_rows = tile_rows(a, t1 + kE, end);
+    }
+    const float* buf = s_tile + (t & 1) * T::kFloats;
+    const float* sx = buf;
+    const float* sg = buf + T::kX;
+    const float* sy = buf + 2 * T::kX;
+    static_for<kWaves>([&](auto wc) __attribute__((always_inline)) {
+      constexpr int w = decltype(wc)::value;
+      constexpr int q0 = w * NPW;
+      constexpr int np = P - q0 < NPW ? P - q0 : NPW;
+      if constexpr (np > 0) {
+        if (wave == w) {
+#pragma unroll 2
+          for (int s = 0; s < kE / 4; ++s) {
+            const int edge = 4 * s + g;
+            int coef_off = 0;
+            asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
+            const float* cf = s_coef + coef_off;
+            float xv[Plan::kComps1], gv[Plan::kComps1], yv[Plan::kComps2];
+            static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
+              constexpr int e = decltype(ec)::value;
+              constexpr REntry E = Plan::e1[e];
+              constexpr bool use_x = wgt_uses<Plan, 0>(q0, np, e);
+              constexpr bool use_g = wgt_uses<Plan, 2>(q0, np, e);
+              static_for<E.dim>([&](auto dc) __attribute__((always_inline)) {
+                constexpr int d = decltype(dc)::value;
+                const int o = edge * T::kXS + 16 * E.base + j * E.dim + d;
+                if constexpr (use_x) xv[E.base + d] = sx[o];
+                if constexpr (use_g) gv[E.base + d] = sg[o];
+              });
+            });
+            static_for<Plan::kEntries2>([&](auto ec) __attribute__((always_inline)) {
+              constexpr int e = decltype(ec)::value;
+              constexpr REntry E = Plan::e2[e];
+              if constexpr (wgt_uses<Plan, 1>(q0, np, e))
+                static_for<E.dim>([&](auto dc) __attribute__((always_inline)) {
+                  constexpr int d = decltype(dc)::value;
+                  yv[E.base + d] = sy[edge * T::kYS + E.base + d];
+                });
+            });
+            static_for<np>([&](auto qc) __attribute__((always_inline)) {
+              constexpr int q = decltype(qc)::value;
+              constexpr int p = Plan::wgt[q0 + q];
+              constexpr RPath ps = Plan::paths[p];
+              constexpr REntry X = Plan::e1[ps.i];
+              constexpr REntry Y = Plan::e2[ps.j];
+              constexpr REntry O = Plan::e1[ps.k];
+              const auto cfs = load_coefs<ps.mask>(cf, p);
+              static_for<8>([&](auto sc) __attribute__((always_inline)) {
+                constexpr int slot = decltype(sc)::value;
+                constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
+                if constexpr ((ps.mask >> slot) & 1)
+                  acc[q] += coef_at<slot>(cfs) * yv[Y.base + ib] *
+                            (xv[X.base + ia] * gv[O.base + c]);
+              });
+            });
+          }
+        }
+      }
+    });
+    if (more) weight_commit<TP, KH>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
+    __syncthreads();
+  }
+
+  float* dst = part + (int64_t)blockIdx.x * P * a.C;
+  static_for<kWaves>([&](auto wc) __attribute__((always_inline)) {
+    constexpr int w = decltype(wc)::value;
+    constexpr int q0 = w * NPW;
+    constexpr int np = P - q0 < NPW ? P - q0 : NPW;
+    if constexpr (np > 0) {
+      if (wave == w) {
+        static_for<np>([&](auto qc) __attribute__((always_inline)) {
+          constexpr int q = decltype(qc)::value;
+          float v = acc[q];
+          v += __shfl_xor(v, 16);
+          v += __shfl_xor(v, 32);
+          if (g == 0) dst[(int64_t)Plan::wgt[q0 + q] * a.C + u0 + j] = v;
         });
       }
     }
