@@ -69,6 +69,9 @@ def _args():
     p.add_argument("--torch-gather", action="store_true",
                    help="radial workload: gather node features with torch indexing (atomic "
                         "scatter-add backward) instead of the fused left_index gather")
+    p.add_argument("--channels-in2", type=int, default=1,
+                   help="uvu-shared workload: copies V of the second input (default 1; with "
+                        "V > 1 the shape is C128 m4 full, 65,536 rows unless --rows is given)")
     p.add_argument("--uvu-rows", type=int, default=16384,
                    help="uvu workload: rows (65536 needs 524 GB of per-row weights)")
     return p.parse_args()
@@ -358,17 +361,27 @@ def uvu_main(args):
 
 def uvu_shared_main(args):
     """UvuTensorProduct in the reference's default mode (shared trainable
-    weights), V = 1: the example of its docs/UVU.md (C128, m6, full first
-    input, canonical second input, 16,384 rows), compiled, forward + gradients
-    of x, y and the weights with a ones cotangent.  Not a BASELINE metric."""
+    weights), compiled, forward + gradients of x, y and the weights with a ones
+    cotangent.  V = 1: the example of its docs/UVU.md (C128, m6, full first
+    input, canonical second input, 16,384 rows).  V = --channels-in2 > 1: C128,
+    m4, full parity, 65,536 rows.  Not a BASELINE metric."""
     import torch
     from ictc_o2_hp import UvuTensorProduct, _native
 
     device = torch.device("cuda:0")
     _native.library()
-    n = args.rows if args.rows != 131072 else 16384
+    v = args.channels_in2
     torch.manual_seed(7)
-    module = UvuTensorProduct(128, 1, 6, parity="full", parity_in2="canonical").to(device)
+    if v == 1:
+        n = args.rows if args.rows != 131072 else 16384
+        module = UvuTensorProduct(128, 1, 6, parity="full", parity_in2="canonical").to(device)
+        shape = "C128 V1 m6 full/canonical"
+        metric = "uvu shared-weight V=1 fwd + VJP rows/s (docs/UVU.md example shape)"
+    else:
+        n = args.rows if args.rows != 131072 else 65536
+        module = UvuTensorProduct(128, v, 4, parity="full").to(device)
+        shape = f"C128 V{v} m4 full"
+        metric = f"uvu shared-weight V={v} fwd + VJP rows/s"
     x = torch.randn(n, module.input1_dimension, device=device, requires_grad=True)
     y = torch.randn(n, module.input2_dimension, device=device, requires_grad=True)
     cot = torch.ones_like(x)
@@ -383,15 +396,15 @@ def uvu_shared_main(args):
     per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in ("uvu_forward", "uvu_backward")}
     alg_fwd, alg_bwd = 4.0 * n * (2 * w1 + w2), 4.0 * n * (3 * w1 + 2 * w2)
     record = {
-        "metric": "uvu shared-weight V=1 fwd + VJP rows/s (docs/UVU.md example shape)",
+        "metric": metric,
         "value": n / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: x, y ~ N(0,1) (seeded), default-initialised shared weights, "
                 "ones cotangent",
-        "config": {"workload": f"UvuTensorProduct C128 V1 m6 full/canonical shared weights "
-                               f"N={n} fwd+VJP (x, y, w)", "rows": n,
-                   "paths": module.weight_numel // 128},
+        "config": {"workload": f"UvuTensorProduct {shape} shared weights N={n} fwd+VJP "
+                               f"(x, y, w)", "rows": n,
+                   "paths": module.weight_numel // (128 * v)},
         "ms_per_step_median": median, "ms_per_step_iqr": iqr, "wall_ms_per_step": wall_ms,
         "kernels_ms": {"forward": per["uvu_forward"], "backward": per["uvu_backward"]},
         "kernels_GBps": {"forward": alg_fwd / (per["uvu_forward"] * 1e-3) / 1e9

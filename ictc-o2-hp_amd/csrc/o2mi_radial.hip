@@ -16,6 +16,7 @@ const o2mi::radial::KernelSet* o2mi_find_radial_set(int m_max, int full, int m_m
 struct o2mi_radial_plan {
   const o2mi::radial::KernelSet* set;
   int C, H;
+  int V;  // copies of the second input (shared-weight uvu plans; 1 otherwise)
   int64_t W1, W2;
 };
 
@@ -137,6 +138,7 @@ Args make_args(const o2mi_radial_plan* p, int64_t n, const float* x, const float
   a.H = p->H;
   a.W1 = (int)p->W1;
   a.W2 = (int)p->W2;
+  a.V = p->V;
   a.x = x;
   a.y = y;
   a.hidden = hidden;
@@ -277,14 +279,33 @@ int radial_backward(const o2mi_radial_plan* plan, const Args& a, const float* gr
   return O2MI_OK;
 }
 
-// Shared-weight V = 1 uvu backward workspace: the dW slice partials, then the
-// split dy partials.
+// Edge slices of the V >= 2 shared-weight gradient kernel: about one block
+// (slice x channel tile x path group) per CU, whole staged tiles per slice.
+void vdw_slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
+  const int64_t blocks_per_slice = (int64_t)(p->C / 16) * p->set->vshared->dw_groups;
+  const int64_t want =
+      std::max<int64_t>(1, (device_cus() + blocks_per_slice - 1) / blocks_per_slice);
+  const int64_t tile = p->set->vshared->dw_edges;
+  const int64_t edge_tiles = std::max<int64_t>(1, (n + tile - 1) / tile);
+  const int64_t s0 = std::min(want, edge_tiles);
+  const int64_t per = ((edge_tiles + s0 - 1) / s0) * tile;
+  *per_slice = per;
+  *slices = (int)std::max<int64_t>(1, (n + per - 1) / per);
+}
+
+void shared_slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
+  if (p->V == 1) dw_slicing(p, n, per_slice, slices);
+  else vdw_slicing(p, n, per_slice, slices);
+}
+
+// Shared-weight uvu backward workspace: the dw slice partials ([slices][P *
+// C * V]), then the split dy partials.
 int64_t shared_dw_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
   if (!(needed & 4) || n <= 0) return 0;
   int64_t per = 0;
   int slices = 0;
-  dw_slicing(p, n, &per, &slices);
-  return (int64_t)slices * p->set->paths * p->C;
+  shared_slicing(p, n, &per, &slices);
+  return (int64_t)slices * p->set->paths * p->C * p->V;
 }
 
 }  // namespace
@@ -309,6 +330,7 @@ int o2mi_radial_plan_create(int channels, int m_max, int parity, int m_max_in2, 
   p->set = set;
   p->C = channels;
   p->H = hidden;
+  p->V = 1;
   p->W1 = (int64_t)channels * set->comps1;
   p->W2 = set->comps2;
   *plan = p;
@@ -375,15 +397,17 @@ int o2mi_radial_backward_gather_f32(const o2mi_radial_plan* plan, const float* x
                          workspace_bytes, needed, stream);
 }
 
-int o2mi_uvu_shared_plan_create(int channels, int m_max, int parity, int m_max_in2,
-                                int parity_in2, o2mi_radial_plan** plan) {
+int o2mi_uvu_shared_plan_create(int channels, int channels_in2, int m_max, int parity,
+                                int m_max_in2, int parity_in2, o2mi_radial_plan** plan) {
   if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
   *plan = nullptr;
-  if (channels < 1 || m_max < 0 || m_max_in2 < 0 || (parity != 0 && parity != 1) ||
-      (parity_in2 != 0 && parity_in2 != 1))
+  if (channels < 1 || channels_in2 < 1 || m_max < 0 || m_max_in2 < 0 ||
+      (parity != 0 && parity != 1) || (parity_in2 != 0 && parity_in2 != 1))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid uvu plan arguments");
   if (channels % 16 != 0)
     return fail(O2MI_ERR_UNSUPPORTED, "shared-weight uvu kernels need channels % 16 == 0");
+  if (channels_in2 > o2mi::radial::kVK)
+    return fail(O2MI_ERR_UNSUPPORTED, "shared-weight uvu kernels need channels_in2 <= 8");
   const KernelSet* set = o2mi_find_radial_set(m_max, parity, m_max_in2, parity_in2, 16);
   if (!set)
     return fail(O2MI_ERR_UNSUPPORTED, "no shared-weight uvu kernel compiled for this structure");
@@ -391,8 +415,9 @@ int o2mi_uvu_shared_plan_create(int channels, int m_max, int parity, int m_max_i
   p->set = set;
   p->C = channels;
   p->H = 0;
+  p->V = channels_in2;
   p->W1 = (int64_t)channels * set->comps1;
-  p->W2 = set->comps2;
+  p->W2 = (int64_t)channels_in2 * set->comps2;
   *plan = p;
   return O2MI_OK;
 }
@@ -408,7 +433,8 @@ int o2mi_uvu_shared_forward_f32(const o2mi_radial_plan* plan, const float* x, co
   const hipStream_t s = static_cast<hipStream_t>(stream);
   O2miTimed timed;
   const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
-  const hipError_t err = plan->set->shared_forward(a, out, s);
+  const hipError_t err = plan->V == 1 ? plan->set->shared_forward(a, out, s)
+                                      : plan->set->vshared->forward(a, out, s);
   if (timing) o2mi_timing_end(s, &timed);
   return err == hipSuccess ? O2MI_OK : fail_hip(err, "shared uvu forward launch");
 }
@@ -430,7 +456,7 @@ int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan* plan, const float* x, c
   if ((needed & 4) && !gweight)
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL weight gradient for a requested role");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t wn = (int64_t)plan->set->paths * plan->C;
+  const int64_t wn = (int64_t)plan->set->paths * plan->C * plan->V;
   if (n_rows == 0) {
     if (needed & 4)
       hipLaunchKernelGGL(zero_kernel, dim3(blocks_for(wn)), dim3(256), 0, s, gweight, wn);
@@ -456,7 +482,9 @@ int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan* plan, const float* x, c
     const int splits = stream_splits(plan, n_rows);
     if (splits > 1 && (needed & 2))
       a.part_dy = static_cast<float*>(workspace) + dw_floats;
-    hipError_t err = plan->set->shared_backward(a, grad_output, gx, gy, needed & 3, s);
+    hipError_t err =
+        plan->V == 1 ? plan->set->shared_backward(a, grad_output, gx, gy, needed & 3, s)
+                     : plan->set->vshared->backward(a, grad_output, gx, gy, needed & 3, s);
     if (err != hipSuccess) return fail_hip(err, "shared uvu backward launch");
     if (a.part_dy)
       hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n_rows * plan->W2)), dim3(256), 0, s,
@@ -465,9 +493,10 @@ int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan* plan, const float* x, c
   if (needed & 4) {
     int64_t per = 0;
     int slices = 0;
-    dw_slicing(plan, n_rows, &per, &slices);
+    shared_slicing(plan, n_rows, &per, &slices);
     float* part = static_cast<float*>(workspace);
-    hipError_t err = plan->set->shared_dw(a, grad_output, per, slices, part, s);
+    hipError_t err = plan->V == 1 ? plan->set->shared_dw(a, grad_output, per, slices, part, s)
+                                  : plan->set->vshared->dw(a, grad_output, per, slices, part, s);
     if (err != hipSuccess) return fail_hip(err, "shared uvu weight-gradient launch");
     hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(wn)), dim3(256), 0, s, part, slices, wn,
                        gweight);

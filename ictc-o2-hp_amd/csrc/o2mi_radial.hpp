@@ -86,6 +86,7 @@ struct Args {
   int H;      // hidden width (multiple of 4, <= 4*KH)
   int W1;     // C * components of the first input
   int W2;     // width of the second input
+  int V;      // copies of the second input (shared-weight uvu; 1 otherwise)
   const float* x;
   const float* y;
   const float* hidden;

@@ -5,9 +5,22 @@
 
 #include "o2mi_radial.hpp"
 #include "o2mi_radial_streamed.hpp"
+#include "o2mi_uvu_vshared.hpp"
 
 namespace o2mi {
 namespace radial {
+
+// The uvu product with shared weights and 2 <= V <= 8 (Args::alpha = weights
+// [P][C][V], Args::V = V).
+struct VSharedLaunchers {
+  int dw_edges;   // edges per staged tile of the weight-gradient kernel
+  int dw_groups;  // path groups (grid z) of the weight-gradient kernel
+  hipError_t (*forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*backward)(const Args&, const float* gout, float* gx, float* gy, int needed,
+                         hipStream_t);
+  hipError_t (*dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
+                   float* part, hipStream_t);
+};
 
 struct KernelSet {
   int paths;
@@ -29,6 +42,7 @@ struct KernelSet {
                                 int needed, hipStream_t);
   hipError_t (*shared_dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
                           float* part, hipStream_t);
+  const VSharedLaunchers* vshared;
 };
 
 static_assert(kSFwdWaves == kSBwdWaves, "forward and input adjoints share one edge blocking");
@@ -95,6 +109,38 @@ hipError_t launch_shared_dw(const Args& a, const float* gout, int64_t edges_per_
 }
 
 template <class Plan>
+hipError_t launch_vshared_forward(const Args& a, float* out, hipStream_t s) {
+  hipLaunchKernelGGL((uvu_vshared_forward_kernel<Plan>), stream_grid(a), dim3(64 * kSFwdWaves), 0,
+                     s, a, out);
+  return hipGetLastError();
+}
+
+template <class Plan>
+hipError_t launch_vshared_backward(const Args& a, const float* gout, float* gx, float* gy,
+                                   int needed, hipStream_t s) {
+  hipLaunchKernelGGL((uvu_vshared_backward_kernel<Plan>), stream_grid(a), dim3(64 * kSBwdWaves),
+                     0, s, a, gout, gx, gy, needed & 3);
+  return hipGetLastError();
+}
+
+template <class Plan>
+hipError_t launch_vshared_dw(const Args& a, const float* gout, int64_t edges_per_slice,
+                             int slices, float* part, hipStream_t s) {
+  hipLaunchKernelGGL((uvu_vshared_dw_kernel<Plan>),
+                     dim3((unsigned)slices, (unsigned)(a.C / 16), (unsigned)vdw_groups<Plan>()),
+                     dim3(kThreads), 0, s, a, gout, edges_per_slice, part);
+  return hipGetLastError();
+}
+
+template <class Plan>
+const VSharedLaunchers* vshared_launchers() {
+  static const VSharedLaunchers l = {vdw_edges<Plan>(), vdw_groups<Plan>(),
+                                     &launch_vshared_forward<Plan>,
+                                     &launch_vshared_backward<Plan>, &launch_vshared_dw<Plan>};
+  return &l;
+}
+
+template <class Plan>
 constexpr int weight_groups() {
   if constexpr (Plan::kWgtStreamed) return wgt_groups<Plan>();
   else return 1;
@@ -120,12 +166,12 @@ const SharedLaunchers* shared_launchers() {
 }
 
 template <class Plan, int KH>
-const KernelSet* kernel_set(const SharedLaunchers* shared) {
+const KernelSet* kernel_set(const SharedLaunchers* shared, const VSharedLaunchers* vshared) {
   static const KernelSet set = {Plan::kPaths, Plan::kComps1, Plan::kComps2, KH,
                                 Plan::kWeightEdges, weight_groups<Plan>(), kStreamEdges,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>, dw_edges<Plan, KH>(),
-                                shared->forward, shared->backward, shared->dw};
+                                shared->forward, shared->backward, shared->dw, vshared};
   return &set;
 }
 
@@ -134,12 +180,18 @@ const KernelSet* kernel_set(const SharedLaunchers* shared) {
 
 #define O2MI_DEFINE_RADIAL_SET(NAME, KH)                                                \
   const o2mi::radial::SharedLaunchers* o2mi_uvu_shared_##NAME##_##KH();                  \
+  const o2mi::radial::VSharedLaunchers* o2mi_uvu_vshared_##NAME##_##KH();                \
   const o2mi::radial::KernelSet* o2mi_radial_set_##NAME##_##KH() {                      \
     return o2mi::radial::kernel_set<o2mi::radial::plans::NAME, KH>(                     \
-        o2mi_uvu_shared_##NAME##_##KH());                                               \
+        o2mi_uvu_shared_##NAME##_##KH(), o2mi_uvu_vshared_##NAME##_##KH());             \
   }
 
 #define O2MI_DEFINE_UVU_SHARED(NAME, KH)                                                \
   const o2mi::radial::SharedLaunchers* o2mi_uvu_shared_##NAME##_##KH() {                \
     return o2mi::radial::shared_launchers<o2mi::radial::plans::NAME, KH>();              \
+  }
+
+#define O2MI_DEFINE_UVU_VSHARED(NAME, KH)                                               \
+  const o2mi::radial::VSharedLaunchers* o2mi_uvu_vshared_##NAME##_##KH() {              \
+    return o2mi::radial::vshared_launchers<o2mi::radial::plans::NAME>();                 \
   }

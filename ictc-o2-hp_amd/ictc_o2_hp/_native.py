@@ -92,7 +92,7 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                     fp, fp, fp, fp, fp, vp, c_sz, c_i64, c_int,
                                                     vp]
     lib.o2mi_uvu_shared_plan_create.restype = c_int
-    lib.o2mi_uvu_shared_plan_create.argtypes = [c_int, c_int, c_int, c_int, c_int,
+    lib.o2mi_uvu_shared_plan_create.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int,
                                                 ctypes.POINTER(vp)]
     lib.o2mi_uvu_shared_forward_f32.restype = c_int
     lib.o2mi_uvu_shared_forward_f32.argtypes = [vp, fp, fp, fp, fp, fp, c_i64, vp]

@@ -201,15 +201,18 @@ int o2mi_radial_backward_gather_f32(const o2mi_radial_plan *plan, const float *x
                                     float *dbias, void *workspace, size_t workspace_bytes,
                                     int64_t n_rows, int needed, void *stream);
 
-/* ---- V = 1 uvu product with shared weights ---------------------------------
- * UvuTensorProduct(C, 1, m, parity=..., parity_in2=..., shared_weights=True),
+/* ---- uvu product with shared weights, 1 <= V <= 8 ---------------------------
+ * UvuTensorProduct(C, V, m, parity=..., parity_in2=..., shared_weights=True),
  * the reference's default weight mode: out[k, u] += sum over paths (i, j, k)
- * of w[p, u] * CG_p(x[i, u], y[j]) (uvu_o2.py:50-73).  Layouts as the radial
- * calls above, weights [P*C] in [path, channel] order.  Plans exist for the
- * same structures as the radial plans (C % 16 == 0, m_max = m_max_in2 <= 6);
- * destroy with o2mi_radial_plan_destroy. */
-int o2mi_uvu_shared_plan_create(int channels, int m_max, int parity, int m_max_in2,
-                                int parity_in2, o2mi_radial_plan **plan);
+ * of CG_p(x[i, u], sum_v w[p, u, v] y[j, v]) (uvu_o2.py:50-73).  Layouts as
+ * the uvu calls above (uvu_o2.py:27-41): x [n][C * components], y [n][V *
+ * components] (entry-major, [copy][component] inside an entry), weights
+ * [P*C*V] in [path, channel, copy] order.  Plans exist for the same
+ * structures as the radial plans (C % 16 == 0, m_max = m_max_in2 <= 6) and
+ * channels_in2 = V <= 8 (O2MI_ERR_UNSUPPORTED otherwise: use the
+ * o2mi_uvu_* calls); destroy with o2mi_radial_plan_destroy. */
+int o2mi_uvu_shared_plan_create(int channels, int channels_in2, int m_max, int parity,
+                                int m_max_in2, int parity_in2, o2mi_radial_plan **plan);
 
 /* out = uvu(x, y; w).  Replaces the uvu forward op for this mode
  * (uvu_triton.py:235-284). */

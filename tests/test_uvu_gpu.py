@@ -104,6 +104,50 @@ def test_uvu_shared_v1_roles_and_reproducible():
     assert normalized_error(first.double().cpu().numpy(), halves.double().cpu().numpy()) <= TOL
 
 
+# 2 <= V <= 8 with shared weights: the v projection, dy and dw on the matrix
+# cores (o2mi_uvu_vshared.hpp).
+SHARED_V = [
+    (16, 2, 2, {"parity": "canonical"}, 300),
+    (32, 3, 4, {"parity": "full"}, 200),
+    (128, 8, 4, {"parity": "full"}, 129),                                 # channels split
+    (48, 5, 3, {"parity": "canonical", "parity_in2": "full", "path_normalization": "path"}, 70),
+    (16, 7, 1, {"parity": "full", "normalization": "norm"}, 1),
+    (32, 4, 6, {"parity": "full", "parity_in2": "canonical"}, 257),
+    (64, 8, 6, {"parity": "full"}, 40),                                   # 508 paths
+    (16, 6, 0, {"parity": "full"}, 33),
+]
+
+
+@pytest.mark.parametrize("c,v,m,kw,n", SHARED_V)
+def test_uvu_shared_v_kernels(c, v, m, kw, n):
+    from ictc_o2_hp import UvuTensorProduct, uvu_ops
+    _case(c, v, m, kw, True, n, seed=c + v + m + n)
+    module = UvuTensorProduct(c, v, m, shared_weights=True, **kw)
+    assert uvu_ops.shared_plan(module._kernel_metadata_id) is not None
+
+
+def test_uvu_shared_v_roles_and_reproducible():
+    from ictc_o2_hp import UvuTensorProduct, uvu_ops
+    for wrt in ((True, False, False), (False, True, False), (False, False, True),
+                (False, True, True)):
+        _case(64, 4, 4, {"parity": "full"}, True, 90, seed=11, wrt=wrt)
+    torch.manual_seed(12)
+    module = UvuTensorProduct(32, 8, 5, parity="full", parity_in2="canonical").cuda()
+    assert uvu_ops.shared_plan(module._kernel_metadata_id) is not None
+    x = torch.randn(40000, module.input1_dimension, device="cuda")
+    y = torch.randn(40000, module.input2_dimension, device="cuda")
+    g = torch.randn_like(x)
+    first = torch.autograd.grad(module(x, y), module.weight, g)[0]
+    second = torch.autograd.grad(module(x, y), module.weight, g)[0]
+    assert torch.equal(first, second)
+    halves = sum(torch.autograd.grad(module(x[s:s + 20000], y[s:s + 20000]), module.weight,
+                                     g[s:s + 20000])[0] for s in (0, 20000))
+    assert normalized_error(first.double().cpu().numpy(), halves.double().cpu().numpy()) <= TOL
+    # V above the kernels' 8 copies keeps the generic kernels.
+    wide = UvuTensorProduct(16, 9, 2, parity="full")
+    assert uvu_ops.shared_plan(wide._kernel_metadata_id) is None
+
+
 @pytest.mark.parametrize("wrt", [(True, False, False), (False, True, False), (False, False, True),
                                  (True, False, True)])
 def test_uvu_gradient_roles(wrt):
