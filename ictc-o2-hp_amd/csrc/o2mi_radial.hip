@@ -279,12 +279,13 @@ int radial_backward(const o2mi_radial_plan* plan, const Args& a, const float* gr
   return O2MI_OK;
 }
 
-// Edge slices of the V >= 2 shared-weight gradient kernel: about one block
-// (slice x channel tile x path group) per CU, whole staged tiles per slice.
+// Edge slices of the V >= 2 shared-weight gradient kernel: at most one block
+// (slice x channel tile x path group) per CU — one block fills a CU, so a
+// block more than the CUs would run as a second round — whole staged tiles
+// per slice.
 void vdw_slicing(const o2mi_radial_plan* p, int64_t n, int64_t* per_slice, int* slices) {
   const int64_t blocks_per_slice = (int64_t)(p->C / 16) * p->set->vshared->dw_groups;
-  const int64_t want =
-      std::max<int64_t>(1, (device_cus() + blocks_per_slice - 1) / blocks_per_slice);
+  const int64_t want = std::max<int64_t>(1, device_cus() / blocks_per_slice);
   const int64_t tile = p->set->vshared->dw_edges;
   const int64_t edge_tiles = std::max<int64_t>(1, (n + tile - 1) / tile);
   const int64_t s0 = std::min(want, edge_tiles);

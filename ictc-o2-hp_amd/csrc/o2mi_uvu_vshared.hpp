@@ -9,7 +9,7 @@
 // h] alpha[h, p, u] with K = V instead of H, so it runs on the fp32 matrix
 // cores in the same lane layout: lane (g, j) holds channels u0+4g .. +3 of
 // edge j.  The weights [P][C][V] are streamed through LDS per channel tile in
-// double-buffered chunks of Plan::kChunk paths, zero-padded to kVK = 8
+// double-buffered chunks of kVChunk paths, zero-padded to kVK = 8
 // copies; the lane's copies 2g, 2g+1 of every second-input component of its
 // edge are the B operands (zero past V).  The input adjoints form dy[e, v, c]
 // = sum_u gz_c[e, u] w[p, u, v] as matrix products over the channels, two
@@ -25,6 +25,14 @@ namespace o2mi {
 namespace radial {
 
 constexpr int kVK = 8;  // copies of the second input a kernel covers (zero-padded)
+
+#ifndef O2MI_VCHUNK
+#define O2MI_VCHUNK 32
+#endif
+// Paths per staged weight chunk: a path costs only 2 MFMAs per second-input
+// component here, so chunks are deeper than the radial kernels' to amortise
+// the chunk barrier.
+constexpr int kVChunk = O2MI_VCHUNK;
 
 // Entry of the V = 1 second-input component c.
 template <class Plan>
@@ -42,11 +50,11 @@ __device__ __forceinline__ int y_offset(int V, int v) {
   return V * E.off + v * E.dim + (c - E.base);
 }
 
-// Weights of Plan::kChunk consecutive paths of an order for channel tile u0,
-// as [slot][16 channels][kVK] (copies >= V zero): global loads in registers.
+// Weights of kVChunk consecutive paths of an order for channel tile u0, as
+// [slot][16 channels][kVK] (copies >= V zero): global loads in registers.
 template <class Plan, int NT>
 struct VChunk {
-  static constexpr int kFloats = Plan::kChunk * 16 * kVK;
+  static constexpr int kFloats = kVChunk * 16 * kVK;
   static constexpr int kPer = (kFloats + NT - 1) / NT;
   static_assert(NT % (16 * kVK) == 0, "a pass covers whole path slots");
   float w[kPer];
@@ -55,7 +63,7 @@ struct VChunk {
 template <class Plan, int NT, bool kBwd, int c>
 __device__ __forceinline__ void vchunk_fetch(VChunk<Plan, NT>& pf, const Args& a, int u0) {
   using S = VChunk<Plan, NT>;
-  constexpr int PC = Plan::kChunk;
+  constexpr int PC = kVChunk;
   constexpr int kSlotsPerPass = NT / (16 * kVK);
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));  // keep the slot -> path selects inside the channel loop
@@ -105,8 +113,8 @@ __device__ __forceinline__ void load_yb(__amdgpu_buffer_rsrc_t ry, const Args& a
 template <class Plan>
 struct VLayout {
   static constexpr int kCoefPad = (Plan::kPaths * 8 + 3) / 4 * 4;
-  static constexpr int kChunks = (Plan::kPaths + Plan::kChunk - 1) / Plan::kChunk;
-  static constexpr int kBufFloats = Plan::kChunk * 16 * kVK;
+  static constexpr int kChunks = (Plan::kPaths + kVChunk - 1) / kVChunk;
+  static constexpr int kBufFloats = kVChunk * 16 * kVK;
   static constexpr int kFloats = kCoefPad + 2 * kBufFloats;
 };
 
@@ -118,7 +126,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void uvu_vshared_forward_kernel
   using L = VLayout<Plan>;
   constexpr int P = Plan::kPaths;
   constexpr int NC = Plan::kComps1;
-  constexpr int PC = Plan::kChunk;
+  constexpr int PC = kVChunk;
   constexpr int NCH = L::kChunks;
   __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
 
@@ -218,7 +226,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void uvu_vshared_backward_kerne
   constexpr int NC = Plan::kComps1;
   constexpr int NY = Plan::kComps2;
   constexpr int NYT = (NY + 1) / 2;  // dy accumulator tiles: components 2t, 2t + 1
-  constexpr int PC = Plan::kChunk;
+  constexpr int PC = kVChunk;
   constexpr int NCH = L::kChunks;
   __shared__ __attribute__((aligned(16))) float s_mem[L::kFloats];
 
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void uvu_vshared_backward_kerne
 }
 
 #ifndef O2MI_VDW_PATHS
-#define O2MI_VDW_PATHS 12
+#define O2MI_VDW_PATHS 16
 #endif
 
 // Weight gradient: paths per wave (at most O2MI_VDW_PATHS) and path groups
