@@ -507,4 +507,66 @@ int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan* plan, const float* x, c
   return err == hipSuccess ? O2MI_OK : fail_hip(err, "shared uvu launch");
 }
 
+int o2mi_uvu_rows_forward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                              const float* weight, const float* coefficients, float* out,
+                              int64_t n_rows, void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (plan->V != 1)
+    return fail(O2MI_ERR_UNSUPPORTED, "per-row weight kernels need a plan with channels_in2 == 1");
+  if (n_rows == 0) return O2MI_OK;
+  if (!x || !y || !weight || !coefficients || !aligned16(x) || !aligned16(out) ||
+      !aligned16(weight))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input or misaligned x / weight / out");
+  Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
+  const hipError_t err = plan->set->row_forward(a, out, s);
+  if (timing) o2mi_timing_end(s, &timed);
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "per-row uvu forward launch");
+}
+
+size_t o2mi_uvu_rows_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
+                                              int needed) {
+  if (!plan || n_rows <= 0 || (needed & ~7)) return 0;
+  return (size_t)split_part_floats(plan, n_rows, needed & 2) * sizeof(float);
+}
+
+int o2mi_uvu_rows_backward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
+                               const float* weight, const float* coefficients,
+                               const float* grad_output, float* gx, float* gy, float* gweight,
+                               void* workspace, size_t workspace_bytes, int64_t n_rows,
+                               int needed, void* stream) {
+  if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "invalid plan or n_rows");
+  if (plan->V != 1)
+    return fail(O2MI_ERR_UNSUPPORTED, "per-row weight kernels need a plan with channels_in2 == 1");
+  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
+  if (n_rows == 0 || needed == 0) return O2MI_OK;
+  if (!x || !y || !weight || !coefficients || !aligned16(x) || !aligned16(weight))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input or misaligned x / weight");
+  if (!grad_output || !aligned16(grad_output))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "grad_output must be a 16-byte aligned pointer");
+  if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy) ||
+      ((needed & 4) && !aligned16(gweight)))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
+  const size_t need = (size_t)split_part_floats(plan, n_rows, needed & 2) * sizeof(float);
+  if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(O2MI_ERR_WORKSPACE,
+                "workspace smaller than o2mi_uvu_rows_backward_workspace_bytes or misaligned");
+  Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int splits = stream_splits(plan, n_rows);
+  if (splits > 1 && (needed & 2)) a.part_dy = static_cast<float*>(workspace);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);
+  hipError_t err = plan->set->row_backward(a, grad_output, gx, gy, gweight, needed, s);
+  if (err != hipSuccess) return fail_hip(err, "per-row uvu backward launch");
+  if (a.part_dy)
+    hipLaunchKernelGGL(slice_sum_kernel, dim3(blocks_for(n_rows * plan->W2)), dim3(256), 0, s,
+                       a.part_dy, splits, n_rows * plan->W2, gy);
+  if (timing) o2mi_timing_end(s, &timed);
+  err = hipGetLastError();
+  return err == hipSuccess ? O2MI_OK : fail_hip(err, "per-row uvu launch");
+}
+
 }  // extern "C"

@@ -43,6 +43,10 @@ struct KernelSet {
   hipError_t (*shared_dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
                           float* part, hipStream_t);
   const VSharedLaunchers* vshared;
+  // The V = 1 uvu product with per-row weights (Args::alpha = weights [n][P*C]).
+  hipError_t (*row_forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*row_backward)(const Args&, const float* gout, float* gx, float* gy, float* gw,
+                             int needed, hipStream_t);
 };
 
 static_assert(kSFwdWaves == kSBwdWaves, "forward and input adjoints share one edge blocking");
@@ -86,7 +90,7 @@ hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_sli
 
 template <class Plan, int KH>
 hipError_t launch_shared_forward(const Args& a, float* out, hipStream_t s) {
-  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, true>), stream_grid(a),
+  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, kSharedW>), stream_grid(a),
                      dim3(64 * kSFwdWaves), 0, s, a, out);
   return hipGetLastError();
 }
@@ -94,8 +98,24 @@ hipError_t launch_shared_forward(const Args& a, float* out, hipStream_t s) {
 template <class Plan, int KH>
 hipError_t launch_shared_backward(const Args& a, const float* gout, float* gx, float* gy,
                                   int needed, hipStream_t s) {
-  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, true>), stream_grid(a),
+  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, kSharedW>), stream_grid(a),
                      dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, nullptr, needed & 3);
+  return hipGetLastError();
+}
+
+template <class Plan, int KH>
+hipError_t launch_row_forward(const Args& a, float* out, hipStream_t s) {
+  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, kRowW>), stream_grid(a),
+                     dim3(64 * kSFwdWaves), 0, s, a, out);
+  return hipGetLastError();
+}
+
+// gw: per-row weight adjoint [n][P*C] (bit 4 of needed).
+template <class Plan, int KH>
+hipError_t launch_row_backward(const Args& a, const float* gout, float* gx, float* gy, float* gw,
+                               int needed, hipStream_t s) {
+  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, kRowW>), stream_grid(a),
+                     dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, gw, needed & 7);
   return hipGetLastError();
 }
 
@@ -155,13 +175,18 @@ struct SharedLaunchers {
                          hipStream_t);
   hipError_t (*dw)(const Args&, const float* gout, int64_t edges_per_slice, int slices,
                    float* part, hipStream_t);
+  // The same product with per-row weights [n][P*C] (Args::alpha).
+  hipError_t (*row_forward)(const Args&, float* out, hipStream_t);
+  hipError_t (*row_backward)(const Args&, const float* gout, float* gx, float* gy, float* gw,
+                             int needed, hipStream_t);
 };
 
 template <class Plan, int KH>
 const SharedLaunchers* shared_launchers() {
   static const SharedLaunchers l = {&launch_shared_forward<Plan, KH>,
                                     &launch_shared_backward<Plan, KH>,
-                                    &launch_shared_dw<Plan, KH>};
+                                    &launch_shared_dw<Plan, KH>, &launch_row_forward<Plan, KH>,
+                                    &launch_row_backward<Plan, KH>};
   return &l;
 }
 
@@ -171,7 +196,8 @@ const KernelSet* kernel_set(const SharedLaunchers* shared, const VSharedLauncher
                                 Plan::kWeightEdges, weight_groups<Plan>(), kStreamEdges,
                                 &launch_forward<Plan, KH>, &launch_backward<Plan, KH>,
                                 &launch_weight<Plan, KH>, dw_edges<Plan, KH>(),
-                                shared->forward, shared->backward, shared->dw, vshared};
+                                shared->forward, shared->backward, shared->dw, vshared,
+                                shared->row_forward, shared->row_backward};
   return &set;
 }
 

@@ -145,10 +145,44 @@ __device__ __forceinline__ void store_zero_entry(__amdgpu_buffer_rsrc_t r, uint3
   store_entry<Dim>(r, row_off, off_c, u, z);
 }
 
-// kShared: the uvu product with shared weights (V = 1): a.alpha holds the
-// [P][C] weights, staged per channel tile instead of generated (no hidden, no
-// bias, no matrix cores).
-template <class Plan, int KH, bool kShared = false>
+// Where the (edge, path, channel) weights come from: kAffineW, generated on
+// the matrix cores from hidden and alpha (the radial product); kSharedW, the
+// uvu product with shared weights (V = 1): a.alpha holds [P][C], staged per
+// channel tile; kRowW, the uvu product with per-row weights (V = 1): a.alpha
+// holds [n][P*C], each lane reading its edge's 4 channels of a path from
+// memory.  The last two have no hidden, no bias and no matrix work.
+constexpr int kAffineW = 0, kSharedW = 1, kRowW = 2;
+
+#ifndef O2MI_ROW_AHEAD
+#define O2MI_ROW_AHEAD 2
+#endif
+// kRowW: a lane's weight loads run this many paths ahead of their use, in a
+// ring of registers refilled per channel tile (position q uses slot q mod
+// kRowAhead; the ring restarts at each tile, one load latency per tile).
+constexpr int kRowAhead = O2MI_ROW_AHEAD;
+
+// Ring slot refill at traversal position q: the weights of position q +
+// kRowAhead of this channel tile.
+template <class Plan, bool kBwd, int q>
+__device__ __forceinline__ void row_refill(f4 (&ring)[kRowAhead], __amdgpu_buffer_rsrc_t rw,
+                                           uint32_t wrow, int C) {
+  constexpr int qn = q + kRowAhead;
+  if constexpr (qn < Plan::kPaths)
+    ring[q % kRowAhead] = ld4(rw, wrow + (uint32_t)(path_at<Plan, kBwd>(qn) * C) * 4u);
+}
+
+// kRowW ring at the start of a channel tile: positions 0 .. kRowAhead-1.
+template <class Plan, bool kBwd>
+__device__ __forceinline__ void row_prologue(f4 (&ring)[kRowAhead], __amdgpu_buffer_rsrc_t rw,
+                                             uint32_t wrow, int C) {
+  static_for<kRowAhead>([&](auto dc) __attribute__((always_inline)) {
+    constexpr int d = decltype(dc)::value;
+    if constexpr (d < Plan::kPaths)
+      ring[d] = ld4(rw, wrow + (uint32_t)(path_at<Plan, kBwd>(d) * C) * 4u);
+  });
+}
+
+template <class Plan, int KH, int kMode = kAffineW>
 __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_kernel(Args a,
                                                                                    float* out) {
   constexpr int NT = 64 * kSFwdWaves;
@@ -169,12 +203,13 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
   const auto rh = rows_rsrc(a.hidden, e0, a.H, rows);
   const auto ro = rows_rsrc(out, e0, a.W1, rows);
+  const auto rw = rows_rsrc(a.alpha, e0, P * a.C, rows);  // kRowW: the rows' weights
   const uint32_t xrow = (uint32_t)(j * a.W1) * 4u;  // edge row (out)
   const uint32_t xsrc = x_row_off(a, e0, rows, j);  // first-input row
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
   float hid[KH];
-  if constexpr (!kShared) load_hidden<KH>(rh, a.H, g, j, hid);
+  if constexpr (kMode == kAffineW) load_hidden<KH>(rh, a.H, g, j, hid);
   float yv[Plan::kComps2];
   static_for<Plan::kComps2>([&](auto cc) __attribute__((always_inline)) {
     constexpr int c = decltype(cc)::value;
@@ -184,18 +219,21 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   const int u_begin = blockIdx.y * a.tile_span;
   const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  if constexpr (!kShared) {
+  if constexpr (kMode == kAffineW) {
     chunk_fetch<Plan, KH, NT, false, 0>(pf, a, u_begin);
     chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   }
+  f4 ring[kRowAhead];
   int parity = 0;  // LDS buffer of the current chunk
   for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
-    if constexpr (kShared) {
+    if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
     const int u = u0 + 4 * g;
+    const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
+    if constexpr (kMode == kRowW) row_prologue<Plan, false>(ring, rw, wrow, a.C);
     float xv[4 * NC];
     load_row<Plan>(rx, xsrc, a.C, u, xv);
     static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
@@ -206,7 +244,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
     float ov[8];
     static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
       constexpr int c = decltype(cc)::value;
-      if constexpr (!kShared) {
+      if constexpr (kMode == kAffineW) {
         if constexpr (c + 1 < NCH) {
           chunk_fetch<Plan, KH, NT, false, c + 1>(pf, a, u0);
         } else {
@@ -232,7 +270,11 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         constexpr bool last = q == P - 1 || Plan::paths[Plan::fwd[q == P - 1 ? q : q + 1]].k != ps.k;
         if constexpr (first) static_for<8>([&](auto ic) __attribute__((always_inline)) { ov[decltype(ic)::value] = 0.f; });
         f4 w;
-        if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        if constexpr (kMode == kSharedW) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        else if constexpr (kMode == kRowW) {
+          w = ring[q % kRowAhead];
+          row_refill<Plan, false, q>(ring, rw, wrow, a.C);
+        }
         else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
         const auto cfs = load_coefs<ps.mask>(cf, p);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
@@ -252,7 +294,7 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
         for (int i = 0; i < 4 * O.dim; ++i) asm volatile("" : "+v"(ov[i]));
         if constexpr (last) store_entry<O.dim>(ro, xrow, O.off * a.C, u, ov);
       });
-      if constexpr (!kShared) {
+      if constexpr (kMode == kAffineW) {
         if (c + 1 < NCH || u0 + 16 < u_end)
           chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
         parity ^= 1;
@@ -262,9 +304,9 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   }
 }
 
-// needed: 1 = x, 2 = y, 4 = hidden (other bits ignored here; kShared: as the
-// forward, no hidden adjoint).
-template <class Plan, int KH, bool kShared = false>
+// needed: 1 = x, 2 = y, 4 = hidden (kAffineW) or the per-row weights (kRowW,
+// written to ghid as [n][P*C]; kSharedW ignores it).
+template <class Plan, int KH, int kMode = kAffineW>
 __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_kernel(
     Args a, const float* gout, float* gx, float* gy, float* ghid, int needed) {
   constexpr int NT = 64 * kSBwdWaves;
@@ -295,10 +337,14 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   float* dy_base = a.part_dy ? a.part_dy + (int64_t)blockIdx.y * a.n * a.W2 : gy;
   const auto rgh = rows_rsrc(a.part_gh ? a.part_gh + (int64_t)blockIdx.y * a.n * a.H : ghid, e0,
                              a.H, (needed & 4) ? rows : 0);
+  // kRowW: the rows' weights, and their adjoint in ghid ([n][P*C]) for bit 4.
+  const auto rw = rows_rsrc(a.alpha, e0, P * a.C, rows);
+  const bool need_w = (needed & 4) != 0;
+  const auto rdw = rows_rsrc(ghid, e0, P * a.C, need_w ? rows : 0);
 
   for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_mem[L::kCoef + idx] = a.coef[idx];
   float hid[KH];
-  if constexpr (!kShared) load_hidden<KH>(rh, a.H, g, j, hid);
+  if constexpr (kMode == kAffineW) load_hidden<KH>(rh, a.H, g, j, hid);
   float yv[NY], dyv[NY];
   static_for<NY>([&](auto cc) __attribute__((always_inline)) {
     constexpr int c = decltype(cc)::value;
@@ -311,18 +357,21 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   const int u_begin = blockIdx.y * a.tile_span;
   const int u_end = u_begin + a.tile_span < a.C ? u_begin + a.tile_span : a.C;
   SChunk<Plan, KH, NT> pf;
-  if constexpr (!kShared) {
+  if constexpr (kMode == kAffineW) {
     chunk_fetch<Plan, KH, NT, true, 0>(pf, a, u_begin);
     chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   }
+  f4 ring[kRowAhead];
   int parity = 0;
   for (int u0 = u_begin; u0 < u_end; u0 += 16) {
     __syncthreads();
-    if constexpr (kShared) {
+    if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
     const int u = u0 + 4 * g;
+    const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
+    if constexpr (kMode == kRowW) row_prologue<Plan, true>(ring, rw, wrow, a.C);
     float gv[4 * NC];
     load_row<Plan>(rg, xrow, a.C, u, gv);
     static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
@@ -339,7 +388,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
     }
     static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
       constexpr int c = decltype(cc)::value;
-      if constexpr (!kShared) {
+      if constexpr (kMode == kAffineW) {
         if constexpr (c + 1 < NCH) {
           chunk_fetch<Plan, KH, NT, true, c + 1>(pf, a, u0);
         } else {
@@ -382,7 +431,11 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
           }
         }
         f4 w;
-        if constexpr (kShared) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        if constexpr (kMode == kSharedW) w = *reinterpret_cast<const f4*>(s_mem + wsh_off + p * 16);
+        else if constexpr (kMode == kRowW) {
+          w = ring[q % kRowAhead];
+          row_refill<Plan, true, q>(ring, rw, wrow, a.C);
+        }
         else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
         float gw[4] = {0.f, 0.f, 0.f, 0.f};
         const auto cfs = load_coefs<ps.mask>(cf, p);
@@ -408,7 +461,10 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
         if constexpr (Y.dim == 2) asm volatile("" : "+v"(dyv[Y.base + 1]));
 #pragma unroll
         for (int i = 0; i < 4 * X.dim; ++i) asm volatile("" : "+v"(dxc[i]));
-        if constexpr (!kShared) {
+        if constexpr (kMode == kRowW) {
+          if (need_w) st4(rdw, f4{gw[0], gw[1], gw[2], gw[3]}, wrow + (uint32_t)(p * a.C) * 4u);
+        }
+        if constexpr (kMode == kAffineW) {
           const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
           static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
             constexpr int t = decltype(tc)::value;
@@ -421,7 +477,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
         if constexpr (last) store_entry<X.dim>(rdx, xrow, X.off * a.C, u, dxc);
         __builtin_amdgcn_sched_barrier(0);
       });
-      if constexpr (!kShared) {
+      if constexpr (kMode == kAffineW) {
         if (c + 1 < NCH || u0 + 16 < u_end)
           chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0 + (parity ^ 1) * L::kBufFloats);
         parity ^= 1;
@@ -441,7 +497,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
     }
   }
-  if constexpr (!kShared)
+  if constexpr (kMode == kAffineW)
     static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
       constexpr int t = decltype(tc)::value;
       const int h = 16 * t + 4 * g;

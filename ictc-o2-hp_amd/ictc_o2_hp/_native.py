@@ -101,6 +101,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_uvu_shared_backward_f32.restype = c_int
     lib.o2mi_uvu_shared_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, fp, vp, c_sz,
                                                  c_i64, c_int, vp]
+    lib.o2mi_uvu_rows_forward_f32.restype = c_int
+    lib.o2mi_uvu_rows_forward_f32.argtypes = [vp, fp, fp, fp, fp, fp, c_i64, vp]
+    lib.o2mi_uvu_rows_backward_workspace_bytes.restype = c_sz
+    lib.o2mi_uvu_rows_backward_workspace_bytes.argtypes = [vp, c_i64, c_int]
+    lib.o2mi_uvu_rows_backward_f32.restype = c_int
+    lib.o2mi_uvu_rows_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, fp, vp, c_sz,
+                                               c_i64, c_int, vp]
     lib.o2mi_rows_gather_f32.restype = c_int
     lib.o2mi_rows_gather_f32.argtypes = [fp, c_i64, vp, c_i64, c_i64, fp, vp]
     lib.o2mi_rows_segment_sum_f32.restype = c_int

@@ -234,6 +234,28 @@ int o2mi_uvu_shared_backward_f32(const o2mi_radial_plan *plan, const float *x, c
                                  void *workspace, size_t workspace_bytes, int64_t n_rows,
                                  int needed, void *stream);
 
+/* ---- V = 1 uvu product with per-row weights -------------------------------
+ * UvuTensorProduct(C, 1, m, ..., shared_weights=False) with external weights
+ * [n][P*C] (uvu_single.py's kernels and uvu_triton.py:235-414 in the
+ * reference).  Takes a plan from o2mi_uvu_shared_plan_create with
+ * channels_in2 == 1 (O2MI_ERR_UNSUPPORTED otherwise); layouts as above.  x,
+ * weight, out, gx, gweight 16-byte aligned. */
+int o2mi_uvu_rows_forward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                              const float *weight, const float *coefficients, float *out,
+                              int64_t n_rows, void *stream);
+
+/* Workspace of o2mi_uvu_rows_backward_f32 (split dy partials when few rows
+ * split the channels; 0 otherwise). */
+size_t o2mi_uvu_rows_backward_workspace_bytes(const o2mi_radial_plan *plan, int64_t n_rows,
+                                              int needed);
+
+/* (gx, gy, gweight [n][P*C]) for the roles in `needed` (1 x, 2 y, 4 weight). */
+int o2mi_uvu_rows_backward_f32(const o2mi_radial_plan *plan, const float *x, const float *y,
+                               const float *weight, const float *coefficients,
+                               const float *grad_output, float *gx, float *gy, float *gweight,
+                               void *workspace, size_t workspace_bytes, int64_t n_rows,
+                               int needed, void *stream);
+
 /* ---- row gather and deterministic row segment sums -------------------------
  * The node <-> edge data movement of a message-passing layer around the
  * radial product.  No counterpart in the reference, which gathers with

@@ -148,6 +148,32 @@ def test_uvu_shared_v_roles_and_reproducible():
     assert uvu_ops.shared_plan(wide._kernel_metadata_id) is None
 
 
+# V = 1 with per-row weights (external weights, as a radial product feeds
+# them): the streamed radial kernels reading each row's weights from memory.
+ROWS_V1 = [
+    (64, 4, {"parity": "canonical"}, 700),                                # configs[4] TP shape
+    (128, 4, {"parity": "full"}, 100),                                    # channels split
+    (32, 6, {"parity": "full", "parity_in2": "canonical"}, 300),
+    (48, 3, {"parity": "canonical", "parity_in2": "full", "path_normalization": "path"}, 70),
+    (16, 0, {"parity": "full", "normalization": "norm"}, 1),
+    (16, 6, {"parity": "full"}, 40),                                      # 508 paths
+]
+
+
+@pytest.mark.parametrize("c,m,kw,n", ROWS_V1)
+def test_uvu_rows_v1_kernels(c, m, kw, n):
+    from ictc_o2_hp import UvuTensorProduct, uvu_ops
+    _case(c, 1, m, kw, False, n, seed=c + m + n + 1)
+    module = UvuTensorProduct(c, 1, m, shared_weights=False, internal_weights=False, **kw)
+    assert uvu_ops._fused_plan(module._kernel_metadata_id, False) is not None
+
+
+def test_uvu_rows_v1_roles():
+    for wrt in ((True, False, False), (False, True, False), (False, False, True),
+                (True, False, True), (False, True, True)):
+        _case(64, 1, 3, {"parity": "full"}, False, 90, seed=13, wrt=wrt)
+
+
 @pytest.mark.parametrize("wrt", [(True, False, False), (False, True, False), (False, False, True),
                                  (True, False, True)])
 def test_uvu_gradient_roles(wrt):
