@@ -100,6 +100,22 @@ int stream_splits(const o2mi_radial_plan* p, int64_t n) {
   return (p->C + span - 1) / span;
 }
 
+// The per-row weight kernels' channel span: as stream_span, for their 64-edge
+// blocks and 32-channel tiles.
+int row_span(const o2mi_radial_plan* p, int64_t n) {
+  const int64_t blocks = std::max<int64_t>(1, (n + kRowStreamEdges - 1) / kRowStreamEdges);
+  const int64_t cus = device_cus();
+  const int tiles = (p->C + 31) / 32;
+  if (blocks >= cus || tiles == 1) return p->C;
+  const int64_t want = std::min<int64_t>(tiles, (cus + blocks - 1) / blocks);
+  return std::min(p->C, 32 * (int)((tiles + want - 1) / want));
+}
+
+int row_splits(const o2mi_radial_plan* p, int64_t n) {
+  const int span = row_span(p, n);
+  return (p->C + span - 1) / span;
+}
+
 // Floats of the affine-adjoint slice partials, then of the split dy / dhidden
 // partials, in the backward workspace.
 int64_t weight_part_floats(const o2mi_radial_plan* p, int64_t n, int needed) {
@@ -518,6 +534,7 @@ int o2mi_uvu_rows_forward_f32(const o2mi_radial_plan* plan, const float* x, cons
       !aligned16(weight))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input or misaligned x / weight / out");
   Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  a.tile_span = row_span(plan, n_rows);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   O2miTimed timed;
   const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
@@ -528,8 +545,9 @@ int o2mi_uvu_rows_forward_f32(const o2mi_radial_plan* plan, const float* x, cons
 
 size_t o2mi_uvu_rows_backward_workspace_bytes(const o2mi_radial_plan* plan, int64_t n_rows,
                                               int needed) {
-  if (!plan || n_rows <= 0 || (needed & ~7)) return 0;
-  return (size_t)split_part_floats(plan, n_rows, needed & 2) * sizeof(float);
+  if (!plan || n_rows <= 0 || (needed & ~7) || !(needed & 2)) return 0;
+  const int splits = row_splits(plan, n_rows);
+  return splits > 1 ? (size_t)splits * n_rows * plan->W2 * sizeof(float) : 0;
 }
 
 int o2mi_uvu_rows_backward_f32(const o2mi_radial_plan* plan, const float* x, const float* y,
@@ -549,13 +567,14 @@ int o2mi_uvu_rows_backward_f32(const o2mi_radial_plan* plan, const float* x, con
   if (((needed & 1) && !aligned16(gx)) || ((needed & 2) && !gy) ||
       ((needed & 4) && !aligned16(gweight)))
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL or misaligned output for a requested gradient");
-  const size_t need = (size_t)split_part_floats(plan, n_rows, needed & 2) * sizeof(float);
+  const size_t need = o2mi_uvu_rows_backward_workspace_bytes(plan, n_rows, needed);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(O2MI_ERR_WORKSPACE,
                 "workspace smaller than o2mi_uvu_rows_backward_workspace_bytes or misaligned");
   Args a = make_args(plan, n_rows, x, y, nullptr, weight, nullptr, coefficients);
+  a.tile_span = row_span(plan, n_rows);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int splits = stream_splits(plan, n_rows);
+  const int splits = row_splits(plan, n_rows);
   if (splits > 1 && (needed & 2)) a.part_dy = static_cast<float*>(workspace);
   O2miTimed timed;
   const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);

@@ -103,9 +103,17 @@ hipError_t launch_shared_backward(const Args& a, const float* gout, float* gx, f
   return hipGetLastError();
 }
 
+// Per-row weights: waves in pairs over 32-channel tiles, 64 edges per block.
+constexpr int kRowStreamEdges = kStreamEdges / 2;
+
+inline dim3 row_grid(const Args& a) {
+  return dim3((unsigned)((a.n + kRowStreamEdges - 1) / kRowStreamEdges),
+              (unsigned)((a.C + a.tile_span - 1) / a.tile_span));
+}
+
 template <class Plan, int KH>
 hipError_t launch_row_forward(const Args& a, float* out, hipStream_t s) {
-  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, kRowW>), stream_grid(a),
+  hipLaunchKernelGGL((radial_forward_streamed_kernel<Plan, KH, kRowW>), row_grid(a),
                      dim3(64 * kSFwdWaves), 0, s, a, out);
   return hipGetLastError();
 }
@@ -114,7 +122,7 @@ hipError_t launch_row_forward(const Args& a, float* out, hipStream_t s) {
 template <class Plan, int KH>
 hipError_t launch_row_backward(const Args& a, const float* gout, float* gx, float* gy, float* gw,
                                int needed, hipStream_t s) {
-  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, kRowW>), stream_grid(a),
+  hipLaunchKernelGGL((radial_backward_streamed_kernel<Plan, KH, kRowW>), row_grid(a),
                      dim3(64 * kSBwdWaves), 0, s, a, gout, gx, gy, gw, needed & 7);
   return hipGetLastError();
 }

@@ -197,7 +197,14 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, j = lane & 15;
-  const int64_t e0 = ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  // kRowW: waves in pairs, one pair per 16 edges; the two waves of a pair take
+  // the two 16-channel halves of a 32-channel tile, so the two halves of each
+  // 128-byte line of a row's weights are read by one CU at about the same time
+  // (one 16-channel tile per pass read every line twice from HBM).
+  const int half = kMode == kRowW ? (wave & 1) : 0;
+  const int64_t e0 = kMode == kRowW
+                         ? ((int64_t)blockIdx.x * (NT / 128) + (wave >> 1)) * kEdgesPerWave
+                         : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
@@ -225,13 +232,14 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   }
   f4 ring[kRowAhead];
   int parity = 0;  // LDS buffer of the current chunk
-  for (int u0 = u_begin; u0 < u_end; u0 += 16) {
+  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
     __syncthreads();
     if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
-    const int u = u0 + 4 * g;
+    if (kMode == kRowW && u0 + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
+    const int u = u0 + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, false>(ring, rw, wrow, a.C);
     float xv[4 * NC];
@@ -322,7 +330,14 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, j = lane & 15;
-  const int64_t e0 = ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  // kRowW: waves in pairs, one pair per 16 edges; the two waves of a pair take
+  // the two 16-channel halves of a 32-channel tile, so the two halves of each
+  // 128-byte line of a row's weights are read by one CU at about the same time
+  // (one 16-channel tile per pass read every line twice from HBM).
+  const int half = kMode == kRowW ? (wave & 1) : 0;
+  const int64_t e0 = kMode == kRowW
+                         ? ((int64_t)blockIdx.x * (NT / 128) + (wave >> 1)) * kEdgesPerWave
+                         : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto rg = rows_rsrc(gout, e0, a.W1, rows);
@@ -363,13 +378,14 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   }
   f4 ring[kRowAhead];
   int parity = 0;
-  for (int u0 = u_begin; u0 < u_end; u0 += 16) {
+  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
     __syncthreads();
     if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
-    const int u = u0 + 4 * g;
+    if (kMode == kRowW && u0 + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
+    const int u = u0 + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, true>(ring, rw, wrow, a.C);
     float gv[4 * NC];
@@ -492,7 +508,17 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       dyv[c] += __shfl_xor(dyv[c], 16);
       dyv[c] += __shfl_xor(dyv[c], 32);
     });
-    if (g == 0 && j < rows) {
+    if constexpr (kMode == kRowW) {
+      static_assert((NT / 128) * 16 * NY <= 2 * L::kBufFloats, "dy exchange fits the buffers");
+      // The pair's second wave hands its channel half's sums to the first.
+      float* s_dy = s_mem + L::kBuf0 + (wave >> 1) * 16 * NY;
+      if (half == 1 && g == 0)
+        static_for<NY>([&](auto cc) __attribute__((always_inline)) { s_dy[j * NY + decltype(cc)::value] = dyv[decltype(cc)::value]; });
+      __syncthreads();
+      if (half == 0)
+        static_for<NY>([&](auto cc) __attribute__((always_inline)) { dyv[decltype(cc)::value] += s_dy[j * NY + decltype(cc)::value]; });
+    }
+    if (g == 0 && j < rows && half == 0) {
       float* dst = dy_base + (e0 + j) * a.W2;
       static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
     }
