@@ -52,7 +52,7 @@ def _args():
     p.add_argument("--no-stream-ceiling", action="store_true",
                    help="skip the HBM streaming-ceiling probe (tp workload)")
     p.add_argument("--workload", default="tp",
-                   choices=("tp", "radial", "uvu", "uvu-shared", "grid", "radial-grid",
+                   choices=("tp", "radial", "uvu", "uvu-rows", "uvu-shared", "grid", "radial-grid",
                             "force"),
                    help="grid: every configs[2] point (and configs[1]) as HIP-graph replays; "
                         "radial-grid: the reference's published radial-chain points; "
@@ -305,20 +305,23 @@ def radial_main(args):
     print(json.dumps(record), flush=True)
 
 
-def uvu_main(args):
+def uvu_main(args, v=32):
     """configs[3] at a row count that fits one GPU: UvuTensorProduct C1=128,
-    C2=32, m4 full, per-row weights N(0, 1/sqrt(C2)), fwd + VJP with dw."""
+    C2=32, m4 full, per-row weights N(0, 1/sqrt(C2)), fwd + VJP with dw.  With
+    v = 1 (workload uvu-rows) the same with one copy of the second input: the
+    per-row weights a radial network feeds (configs[4]'s op with external
+    weights), not a BASELINE metric."""
     import torch
     from ictc_o2_hp import UvuTensorProduct, _native
 
     device = torch.device("cuda:0")
     _native.library()
     n = args.uvu_rows
-    module = UvuTensorProduct(128, 32, 4, parity="full", shared_weights=False).to(device)
+    module = UvuTensorProduct(128, v, 4, parity="full", shared_weights=False).to(device)
     gen = torch.Generator(device=device).manual_seed(3131)
     x = torch.randn((n, module.input1_dimension), device=device, generator=gen)
     y = torch.randn((n, module.input2_dimension), device=device, generator=gen)
-    w = torch.randn((n, module.weight_numel), device=device, generator=gen) / (32 ** 0.5)
+    w = torch.randn((n, module.weight_numel), device=device, generator=gen) / (v ** 0.5)
     for t in (x, y, w):
         t.requires_grad_()
     cot = torch.ones_like(x)
@@ -336,13 +339,16 @@ def uvu_main(args):
     alg_bwd = 4.0 * n * (3 * w1 + 2 * w2 + 2 * pw)
     per = {k: kinds[k][0] / max(1, kinds[k][1]) for k in ("uvu_forward", "uvu_backward")}
     bwd_gbs = alg_bwd / (per["uvu_backward"] * 1e-3) / 1e9 if per["uvu_backward"] else None
+    kernel = "uvu_row_backward_kernel" if v == 32 else "radial_backward_streamed_kernel (per-row)"
     record = {
-        "metric": "uvu fwd + VJP rows/s (configs[3] shape, reduced N); step HBM GB/s",
+        "metric": ("uvu fwd + VJP rows/s (configs[3] shape, reduced N); step HBM GB/s" if v == 32
+                   else f"uvu per-row V={v} fwd + VJP rows/s; step HBM GB/s"),
         "value": n / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic: x, y ~ N(0,1), w ~ N(0, 1/sqrt(32)) per row (seeded), ones cotangent",
-        "config": {"workload": f"UvuTensorProduct C128 V32 m4 full N={n} per-row weights "
+        "data": f"synthetic: x, y ~ N(0,1), w ~ N(0, 1/sqrt({v})) per row (seeded), ones "
+                "cotangent",
+        "config": {"workload": f"UvuTensorProduct C128 V{v} m4 full N={n} per-row weights "
                                "fwd+VJP (x, y, w)", "rows": n, "weights_per_row": pw},
         "ms_per_step_median": median, "ms_per_step_iqr": iqr,
         "wall_ms_per_step": wall_ms,
@@ -350,11 +356,11 @@ def uvu_main(args):
         "kernels_ms": {"forward": per["uvu_forward"], "backward": per["uvu_backward"],
                        "forward_GBps": alg_fwd / (per["uvu_forward"] * 1e-3) / 1e9
                        if per["uvu_forward"] else None},
-        "roofline": {"bound": "hbm", "kernel": "uvu_row_backward_kernel", "achieved": bwd_gbs,
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": bwd_gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": bwd_gbs / HBM_PEAK_GBS if bwd_gbs else None,
                      "traffic": _traffic(REPO / "profiles" / "traffic.json",
-                                         f"uvu_backward_C128_V32_m4_full_N{n}")},
+                                         f"uvu_backward_C128_V{v}_m4_full_N{n}")},
     }
     print(json.dumps(record), flush=True)
 
@@ -753,6 +759,8 @@ def main():
         return force_main(args)
     if args.workload == "uvu-shared":
         return uvu_shared_main(args)
+    if args.workload == "uvu-rows":
+        return uvu_main(args, v=1)
     if args.workload != "tp":
         (radial_main if args.workload == "radial" else uvu_main)(args)
         return _copy_probe(args)
