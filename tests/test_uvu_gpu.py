@@ -204,18 +204,19 @@ def test_uvu_golden_vectors(golden_uvu):
             assert normalized_error(golden_uvu[f"{name}/{key}"], value) <= TOL, (name, key)
 
 
-def test_uvu_empty_rows():
+@pytest.mark.parametrize("c,v,shared", [(8, 2, True), (8, 2, False), (16, 1, True), (16, 2, True),
+                                        (16, 1, False)])
+def test_uvu_empty_rows(c, v, shared):
     from ictc_o2_hp import UvuTensorProduct
-    for shared in (True, False):
-        module = UvuTensorProduct(8, 2, 2, shared_weights=shared, internal_weights=False).cuda()
-        x = torch.zeros(0, module.input1_dimension, device="cuda", requires_grad=True)
-        y = torch.zeros(0, module.input2_dimension, device="cuda", requires_grad=True)
-        w = torch.zeros((module.weight_numel,) if shared else (0, module.weight_numel),
-                        device="cuda", requires_grad=True)
-        out = module(x, y, w)
-        dx, dy, dw = torch.autograd.grad(out, (x, y, w), torch.zeros_like(out))
-        assert out.shape == x.shape and dx.shape == x.shape and dy.shape == y.shape
-        assert dw.shape == w.shape and torch.count_nonzero(dw).item() == 0
+    module = UvuTensorProduct(c, v, 2, shared_weights=shared, internal_weights=False).cuda()
+    x = torch.zeros(0, module.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.zeros(0, module.input2_dimension, device="cuda", requires_grad=True)
+    w = torch.zeros((module.weight_numel,) if shared else (0, module.weight_numel),
+                    device="cuda", requires_grad=True)
+    out = module(x, y, w)
+    dx, dy, dw = torch.autograd.grad(out, (x, y, w), torch.zeros_like(out))
+    assert out.shape == x.shape and dx.shape == x.shape and dy.shape == y.shape
+    assert dw.shape == w.shape and torch.count_nonzero(dw).item() == 0
 
 
 def test_uvu_into_ops_and_internal_weights():
@@ -268,13 +269,16 @@ def test_uvu_double_backward():
     assert normalized_error(hw64.numpy(), hw.double().cpu().numpy()) <= TOL
 
 
-@pytest.mark.parametrize("shared", [False, True])
-def test_uvu_second_and_third_order(shared):
+# C = 8: generic kernels; C = 16: the plan-specialised shared V = 1, V = 2 and
+# per-row V = 1 kernels.
+@pytest.mark.parametrize("c,v,shared", [(8, 2, False), (8, 2, True), (16, 1, True), (16, 2, True),
+                                        (16, 1, False)])
+def test_uvu_second_and_third_order(c, v, shared):
     """Cotangents on all three first-order results, the grad_output term, and
     third order, against the fp64 CPU module."""
     from ictc_o2_hp import UvuTensorProduct
     torch.manual_seed(3)
-    module = UvuTensorProduct(8, 2, 2, parity="full", shared_weights=shared).cuda()
+    module = UvuTensorProduct(c, v, 2, parity="full", shared_weights=shared).cuda()
     n = 21
     x = torch.randn(n, module.input1_dimension, device="cuda", requires_grad=True)
     y = torch.randn(n, module.input2_dimension, device="cuda", requires_grad=True)
@@ -290,9 +294,9 @@ def test_uvu_second_and_third_order(shared):
         t = ha.sum() + hb.square().sum() + hc.sum()
         return (ga, gb, gc, ha, hb, hc) + torch.autograd.grad(t, (a, b, c))
 
-    print(f"case uvu orders 1-3 shared={shared}", flush=True)
+    print(f"case uvu orders 1-3 C={c} V={v} shared={shared}", flush=True)
     got = orders(module, x, y, w)
-    m64 = UvuTensorProduct(8, 2, 2, parity="full", shared_weights=shared).double()
+    m64 = UvuTensorProduct(c, v, 2, parity="full", shared_weights=shared).double()
     x64, y64, w64 = (t.detach().double().cpu().requires_grad_() for t in (x, y, w))
     want = orders(m64, x64, y64, w64)
     for r, a in zip(want, got):
