@@ -621,6 +621,200 @@ __global__ __launch_bounds__(kRowThreads) void uvu_row_backward_kernel(
       gy[n * pr.W2 + i] = (sdy[i] + sdy[pr.W2 + i]) + (sdy[2 * pr.W2 + i] + sdy[3 * pr.W2 + i]);
 }
 
+// ---- Per-row weights, 3 <= V <= 7 not a multiple of 4: one wave per row ----
+// The row-streaming kernels above need V = 4 G.  Here a wave owns a row: its
+// x, y (and g) and the out / dx accumulators live in LDS, and lane l owns the
+// channels l, l + 64, ... for every path (one writer per element), so its V
+// weights of a channel are one contiguous run and the wave's loads of a path
+// one coalesced stream.  Compiled per V; paths are taken wave_batch<V>() at
+// a time (larger batches measured slower: the accumulators are read and
+// written in LDS per path).  dy is summed per second-input entry over the
+// wave's lanes by shuffles, in a fixed order, reading x and g once for all V
+// copies (the generic dy kernel reads them once per copy).  Rows per block =
+// blockDim.x / 64; every wave reaches every barrier.  V = 1 and 2 measured
+// slower here than with the generic kernels and keep those.
+constexpr int kWaveMaxV = 8;
+
+template <int V>
+constexpr int wave_batch() {
+  return 4;
+}
+
+__device__ __forceinline__ float wave_sum_all(float v) {
+  for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+  return v;
+}
+
+template <int V>
+__global__ __launch_bounds__(256) void uvu_wave_forward_kernel(Problem pr,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ y,
+                                                               const float* __restrict__ w,
+                                                               float* __restrict__ out) {
+  extern __shared__ float s_wave[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+  const bool active = n < pr.n;
+  const int per = 2 * pr.W1 + pr.W2;
+  float* sx = s_wave + wave * per;
+  float* so = sx + pr.W1;
+  float* sy = so + pr.W1;
+  if (active) {
+    for (int i = lane; i < pr.W1; i += 64) {
+      sx[i] = x[n * pr.W1 + i];
+      so[i] = 0.f;
+    }
+    for (int i = lane; i < pr.W2; i += 64) sy[i] = y[n * pr.W2 + i];
+  }
+  __syncthreads();
+  if (active) {
+    constexpr int B = wave_batch<V>();
+    const float* wr = w + n * pr.wnum;
+    for (int u = lane; u < pr.C; u += 64) {
+      for (int p0 = 0; p0 < pr.P; p0 += B) {
+        float wv[B][V];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          const int p = p0 + b < pr.P ? p0 + b : pr.P - 1;
+          const float* src = wr + pr.info[7 * p + 6] + (int64_t)u * V;
+#pragma unroll
+          for (int v = 0; v < V; ++v) wv[b][v] = src[v];
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          const int p = p0 + b;
+          if (p >= pr.P) break;
+          const PathRec r = path_rec(pr, p);
+          const float* c = pr.coef + 8 * p;
+          float p0v = 0.f, p1v = 0.f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            p0v = fmaf(wv[b][v], sy[r.yo + v * r.yd], p0v);
+            if (r.yd == 2) p1v = fmaf(wv[b][v], sy[r.yo + v * r.yd + 1], p1v);
+          }
+          const float a0 = sx[r.xo + u * r.xd];
+          const float a1 = r.xd == 2 ? sx[r.xo + u * r.xd + 1] : 0.f;
+          float* o = so + r.oo + u * r.od;
+          o[0] += a0 * (c[0] * p0v + c[1] * p1v) + a1 * (c[2] * p0v + c[3] * p1v);
+          if (r.od == 2) o[1] += a0 * (c[4] * p0v + c[5] * p1v) + a1 * (c[6] * p0v + c[7] * p1v);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (active)
+    for (int i = lane; i < pr.W1; i += 64) out[n * pr.W1 + i] = so[i];
+}
+
+// dx (bit 1), dy (bit 2) and per-row dw (bit 4), paths grouped by
+// second-input entry (second_order).
+template <int V>
+__global__ __launch_bounds__(256) void uvu_wave_backward_kernel(
+    Problem pr, const float* __restrict__ x, const float* __restrict__ y,
+    const float* __restrict__ w, const float* __restrict__ g, float* __restrict__ gx,
+    float* __restrict__ gy, float* __restrict__ gw, int needed) {
+  extern __shared__ float s_wave[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+  const bool active = n < pr.n;
+  const int per = 3 * pr.W1 + 2 * pr.W2;
+  float* sx = s_wave + wave * per;
+  float* sg = sx + pr.W1;
+  float* sdx = sg + pr.W1;
+  float* sy = sdx + pr.W1;
+  float* sdy = sy + pr.W2;
+  if (active) {
+    for (int i = lane; i < pr.W1; i += 64) {
+      sx[i] = x[n * pr.W1 + i];
+      sg[i] = g[n * pr.W1 + i];
+      sdx[i] = 0.f;
+    }
+    for (int i = lane; i < pr.W2; i += 64) sy[i] = y[n * pr.W2 + i];
+  }
+  __syncthreads();
+  const bool want_x = needed & 1, want_y = (needed & 2) != 0, want_w = (needed & 4) != 0;
+  const bool read_w = want_x || want_y;
+  if (active) {
+    constexpr int B = wave_batch<V>();
+    const float* wr = w + n * pr.wnum;
+    float* dwr = want_w ? gw + n * pr.wnum : nullptr;
+    for (int j = 0; j < pr.NY; ++j) {
+      int yo, yd, begin, end;
+      entry_rec(pr, 2, j, yo, yd, begin, end);
+      float dy[V][2];
+#pragma unroll
+      for (int v = 0; v < V; ++v) dy[v][0] = dy[v][1] = 0.f;
+      for (int u = lane; u < pr.C; u += 64) {
+        for (int k0 = begin; k0 < end; k0 += B) {
+          float wv[B][V];
+          if (read_w) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+              const int p = pr.order2[k0 + b < end ? k0 + b : end - 1];
+              const float* src = wr + pr.info[7 * p + 6] + (int64_t)u * V;
+#pragma unroll
+              for (int v = 0; v < V; ++v) wv[b][v] = src[v];
+            }
+          }
+#pragma unroll
+          for (int b = 0; b < B; ++b) {
+            if (k0 + b >= end) break;
+            const int p = pr.order2[k0 + b];
+            const PathRec r = path_rec(pr, p);
+            const float* c = pr.coef + 8 * p;
+            const float a0 = sx[r.xo + u * r.xd];
+            const float a1 = r.xd == 2 ? sx[r.xo + u * r.xd + 1] : 0.f;
+            const float g0 = sg[r.oo + u * r.od];
+            const float g1 = r.od == 2 ? sg[r.oo + u * r.od + 1] : 0.f;
+            // r_b = d out / d proj_b for this (row, path, u).
+            const float r0 = a0 * (c[0] * g0 + c[4] * g1) + a1 * (c[2] * g0 + c[6] * g1);
+            const float r1 = a0 * (c[1] * g0 + c[5] * g1) + a1 * (c[3] * g0 + c[7] * g1);
+            if (want_w) {
+              float* dst = dwr + r.wo + (int64_t)u * V;
+#pragma unroll
+              for (int v = 0; v < V; ++v)
+                dst[v] = yd == 2 ? r0 * sy[yo + 2 * v] + r1 * sy[yo + 2 * v + 1] : r0 * sy[yo + v];
+            }
+            if (read_w) {
+              float p0v = 0.f, p1v = 0.f;
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                dy[v][0] = fmaf(wv[b][v], r0, dy[v][0]);
+                dy[v][1] = fmaf(wv[b][v], r1, dy[v][1]);
+                p0v = fmaf(wv[b][v], sy[yo + v * yd], p0v);
+                if (yd == 2) p1v = fmaf(wv[b][v], sy[yo + v * yd + 1], p1v);
+              }
+              if (want_x) {
+                float* d = sdx + r.xo + u * r.xd;
+                d[0] += g0 * (c[0] * p0v + c[1] * p1v) + g1 * (c[4] * p0v + c[5] * p1v);
+                if (r.xd == 2) d[1] += g0 * (c[2] * p0v + c[3] * p1v) + g1 * (c[6] * p0v + c[7] * p1v);
+              }
+            }
+          }
+        }
+      }
+      if (want_y) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float s0 = wave_sum_all(dy[v][0]);
+          const float s1 = wave_sum_all(dy[v][1]);
+          if (lane == 0) {
+            sdy[yo + v * yd] = s0;
+            if (yd == 2) sdy[yo + v * yd + 1] = s1;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (active) {
+    if (want_x)
+      for (int i = lane; i < pr.W1; i += 64) gx[n * pr.W1 + i] = sdx[i];
+    if (want_y)
+      for (int i = lane; i < pr.W2; i += 64) gy[n * pr.W2 + i] = sdy[i];
+  }
+}
+
 __global__ __launch_bounds__(256) void uvu_column_sum_kernel(const float* __restrict__ in,
                                                              int64_t rows, int64_t cols,
                                                              float* __restrict__ out) {
@@ -689,6 +883,17 @@ size_t row_kernel_lds(const Problem& pr, bool backward, const void* w, const voi
   return bytes <= 65536 ? bytes : 0;
 }
 
+// Rows per block of the wave-per-row kernels (per-row weights, 3 <= V <= 7
+// not a multiple of 4), or 0 when they do not apply: as many rows as the
+// default 64 KB of dynamic LDS holds, up to 4.
+int wave_kernel_rows(const Problem& pr, bool backward) {
+  if (pr.shared || pr.V < 3 || pr.V > kWaveMaxV || pr.V % 4 == 0 || pr.n > 0x7fffffff) return 0;
+  const size_t floats = backward ? (size_t)3 * pr.W1 + (size_t)2 * pr.W2
+                                 : (size_t)2 * pr.W1 + (size_t)pr.W2;
+  const size_t rows = 65536 / (floats * sizeof(float));
+  return (int)std::min<size_t>(rows, 4);
+}
+
 }  // namespace uvu
 }  // namespace o2mi
 
@@ -708,6 +913,21 @@ int o2mi_uvu_forward_f32(const o2mi_uvu_problem* problem, const float* x, const 
     const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
     hipLaunchKernelGGL(uvu_row_forward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
                        pr, x, y, w, out);
+    if (timing) o2mi_timing_end(s, &timed);
+    return hipGetLastError() == hipSuccess ? O2MI_OK
+                                           : fail(O2MI_ERR_HIP, "uvu forward launch failed");
+  }
+  if (const int rows = wave_kernel_rows(pr, false)) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_FORWARD);
+    const size_t lds = (size_t)rows * (2 * pr.W1 + pr.W2) * sizeof(float);
+    const dim3 grid((unsigned)((pr.n + rows - 1) / rows)), block(64 * rows);
+    switch (pr.V) {
+      case 3: hipLaunchKernelGGL(uvu_wave_forward_kernel<3>, grid, block, lds, s, pr, x, y, w, out); break;
+      case 5: hipLaunchKernelGGL(uvu_wave_forward_kernel<5>, grid, block, lds, s, pr, x, y, w, out); break;
+      case 6: hipLaunchKernelGGL(uvu_wave_forward_kernel<6>, grid, block, lds, s, pr, x, y, w, out); break;
+      default: hipLaunchKernelGGL(uvu_wave_forward_kernel<7>, grid, block, lds, s, pr, x, y, w, out); break;
+    }
     if (timing) o2mi_timing_end(s, &timed);
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu forward launch failed");
@@ -752,6 +972,21 @@ int o2mi_uvu_backward_f32(const o2mi_uvu_problem* problem, const float* x, const
     const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);
     hipLaunchKernelGGL(uvu_row_backward_kernel, dim3((unsigned)pr.n), dim3(kRowThreads), lds, s,
                        pr, x, y, w, g, gx, gy, gw, needed);
+    if (timing) o2mi_timing_end(s, &timed);
+    return hipGetLastError() == hipSuccess ? O2MI_OK
+                                           : fail(O2MI_ERR_HIP, "uvu backward launch failed");
+  }
+  if (const int rows = wave_kernel_rows(pr, true)) {
+    O2miTimed timed;
+    const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_UVU_BACKWARD);
+    const size_t lds = (size_t)rows * (3 * pr.W1 + 2 * pr.W2) * sizeof(float);
+    const dim3 grid((unsigned)((pr.n + rows - 1) / rows)), block(64 * rows);
+    switch (pr.V) {
+      case 3: hipLaunchKernelGGL(uvu_wave_backward_kernel<3>, grid, block, lds, s, pr, x, y, w, g, gx, gy, gw, needed); break;
+      case 5: hipLaunchKernelGGL(uvu_wave_backward_kernel<5>, grid, block, lds, s, pr, x, y, w, g, gx, gy, gw, needed); break;
+      case 6: hipLaunchKernelGGL(uvu_wave_backward_kernel<6>, grid, block, lds, s, pr, x, y, w, g, gx, gy, gw, needed); break;
+      default: hipLaunchKernelGGL(uvu_wave_backward_kernel<7>, grid, block, lds, s, pr, x, y, w, g, gx, gy, gw, needed); break;
+    }
     if (timing) o2mi_timing_end(s, &timed);
     return hipGetLastError() == hipSuccess ? O2MI_OK
                                            : fail(O2MI_ERR_HIP, "uvu backward launch failed");

@@ -66,6 +66,25 @@ def test_uvu_parity(c, v, m, kw, shared, n):
     _case(c, v, m, kw, shared, n, seed=c * 100 + v * 10 + m)
 
 
+# Per-row weights with 3 <= V <= 7 not a multiple of 4: one wave per row (and
+# V = 1, 2 through the generic kernels).
+WAVE_ROWS = [
+    (130, 3, 2, {"parity": "full"}, 40),                   # two channel passes per lane
+    (64, 6, 4, {"parity": "canonical", "parity_in2": "full"}, 30),
+    (16, 7, 6, {"parity": "full"}, 9),
+    (96, 5, 3, {"parity": "full", "path_normalization": "path"}, 17),
+    (24, 1, 4, {"parity": "canonical", "normalization": "norm"}, 65),
+    (40, 2, 7, {"parity": "canonical"}, 12),
+]
+
+
+@pytest.mark.parametrize("c,v,m,kw,n", WAVE_ROWS)
+def test_uvu_wave_rows(c, v, m, kw, n):
+    _case(c, v, m, kw, False, n, seed=c * 7 + v + m)
+    for wrt in ((True, False, False), (False, True, False), (False, False, True)):
+        _case(c, v, m, kw, False, 5, seed=c + v, wrt=wrt)
+
+
 # V = 1 with shared weights (the reference's default mode) and m_max_in2 ==
 # m_max: the plan-specialised kernels shared with the radial product.
 SHARED_V1 = [
