@@ -169,3 +169,40 @@ def test_radial_plan_create_validation():
     assert lib.o2mi_radial_plan_create(0, 4, 0, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_plan_create(64, 4, 2, 4, 0, 64, ctypes.byref(handle)) == -1
     assert lib.o2mi_radial_backward_workspace_bytes(None, 10, 31) == 0
+
+
+def test_uvu_plan_create_validation():
+    """Plans of the plan-specialised uvu kernels (shared weights 1 <= V <= 8,
+    per-row weights V = 1) and the argument checks that precede any GPU call."""
+    import ctypes
+    from ictc_o2_hp import _native
+    try:
+        lib = _native.library()
+    except _native.NativeLibraryError:
+        pytest.skip("library not built")
+    handle = ctypes.c_void_p()
+    for v in (1, 2, 3, 8):
+        assert lib.o2mi_uvu_shared_plan_create(64, v, 4, 0, 4, 0, ctypes.byref(handle)) == 0
+        assert lib.o2mi_radial_paths(handle) == 31
+        assert lib.o2mi_radial_plan_destroy(handle) == 0
+    assert lib.o2mi_uvu_shared_plan_create(32, 4, 6, 1, 6, 1, ctypes.byref(handle)) == 0
+    assert lib.o2mi_radial_paths(handle) == 508
+    assert lib.o2mi_radial_plan_destroy(handle) == 0
+    assert lib.o2mi_uvu_shared_plan_create(64, 9, 4, 0, 4, 0, ctypes.byref(handle)) == -2
+    assert lib.o2mi_uvu_shared_plan_create(24, 1, 4, 0, 4, 0, ctypes.byref(handle)) == -2
+    assert lib.o2mi_uvu_shared_plan_create(64, 2, 7, 0, 7, 0, ctypes.byref(handle)) == -2
+    assert lib.o2mi_uvu_shared_plan_create(64, 0, 4, 0, 4, 0, ctypes.byref(handle)) == -1
+    assert lib.o2mi_uvu_shared_plan_create(64, 1, 4, 3, 4, 0, ctypes.byref(handle)) == -1
+    # Per-row weights need V = 1; zero rows are a no-op.
+    v1, v2 = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.o2mi_uvu_shared_plan_create(64, 1, 4, 0, 4, 0, ctypes.byref(v1)) == 0
+    assert lib.o2mi_uvu_shared_plan_create(64, 2, 4, 0, 4, 0, ctypes.byref(v2)) == 0
+    assert lib.o2mi_uvu_rows_forward_f32(v2, None, None, None, None, None, 10, None) == -2
+    assert lib.o2mi_uvu_rows_forward_f32(v1, None, None, None, None, None, 0, None) == 0
+    assert lib.o2mi_uvu_rows_forward_f32(v1, None, None, None, None, None, 10, None) == -1
+    assert lib.o2mi_uvu_rows_backward_f32(v1, None, None, None, None, None, None, None, None,
+                                          None, 0, 10, 8, None) == -1
+    assert lib.o2mi_uvu_rows_backward_f32(v2, None, None, None, None, None, None, None, None,
+                                          None, 0, 10, 7, None) == -2
+    for h in (v1, v2):
+        assert lib.o2mi_radial_plan_destroy(h) == 0
