@@ -161,6 +161,14 @@ constexpr int kAffineW = 0, kSharedW = 1, kRowW = 2;
 // kRowAhead; the ring restarts at each tile, one load latency per tile).
 constexpr int kRowAhead = O2MI_ROW_AHEAD;
 
+// kRowW: cache policy of the per-row weight-adjoint stores.  Default
+// (write-back) lets L2 merge the two halves of a 128-byte line that the two
+// waves of a pair write at about the same time; non-temporal 16-byte stores
+// (2) measured 10% slower.
+#ifndef O2MI_ROW_DW_POLICY
+#define O2MI_ROW_DW_POLICY 0
+#endif
+
 // Ring slot refill at traversal position q: the weights of position q +
 // kRowAhead of this channel tile.
 template <class Plan, bool kBwd, int q>
@@ -478,7 +486,11 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
 #pragma unroll
         for (int i = 0; i < 4 * X.dim; ++i) asm volatile("" : "+v"(dxc[i]));
         if constexpr (kMode == kRowW) {
-          if (need_w) st4(rdw, f4{gw[0], gw[1], gw[2], gw[3]}, wrow + (uint32_t)(p * a.C) * 4u);
+          if (need_w) {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, f4{gw[0], gw[1], gw[2], gw[3]}), rdw,
+                (int)(wrow + (uint32_t)(p * a.C) * 4u), 0, O2MI_ROW_DW_POLICY);
+          }
         }
         if constexpr (kMode == kAffineW) {
           const float* acol = s_mem + acol_off + slot * 16 * G::kRow;
