@@ -127,12 +127,12 @@ def _sample_stats(samples):
 
 def _stream_ceiling(rows, width):
     """Best GB/s of plain 3-read/2-write and 2-read/1-write row streams on this
-    GPU (ictc_o2_hp/o2mi_stream_probe, a child process), or None."""
+    GPU (ictc-o2-hp_amd/bin/o2mi_stream_probe, a child process), or None."""
     import subprocess
-    probe = REPO / "ictc-o2-hp_amd" / "ictc_o2_hp" / "o2mi_stream_probe"
+    probe = REPO / "ictc-o2-hp_amd" / "bin" / "o2mi_stream_probe"
     if not probe.exists():
         return None
-    width = width if width <= 4096 and width % 2 == 0 else 3328
+    width = width if width <= 4096 and width % 4 == 0 else 3328
     try:
         proc = subprocess.run([str(probe), str(rows), str(width)], capture_output=True,
                               text=True, timeout=120)

@@ -27,7 +27,7 @@ from . import __version__
 from . import _native
 from .plan import TPPlan
 
-NAMESPACE = "ictc_o2_hp_amd_v" + __version__.replace(".", "_")
+NAMESPACE = "ictc_o2_hp_v" + __version__.replace(".", "_")
 
 
 @dataclass

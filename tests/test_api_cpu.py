@@ -165,3 +165,51 @@ def test_o2_math_public_functions():
                           atol=1e-12)
     with pytest.raises(ValueError):
         o2_math.o2_cg_tensor("0x", "1", "1")
+
+
+# The reference's op schemas, written out from its signatures
+# (triton_o2.py:786-794, :878-887; uvu_triton.py:267-284, :391-414;
+# radial_streamed.py:81-115).  Namespaces: triton_o2.py:22, uvu_triton.py:12.
+_REFERENCE_SCHEMAS = {
+    ("ictc_o2_hp_v0_1_6_dev0", "o2_forward"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor path_info, "
+        "Tensor path_coefficients, SymInt metadata_id) -> Tensor",
+    ("ictc_o2_hp_v0_1_6_dev0", "o2_backward"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor grad_output, Tensor path_info, "
+        "Tensor path_coefficients, SymInt metadata_id) -> (Tensor, Tensor, Tensor)",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "forward"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor info, Tensor coefficients, "
+        "Tensor first_order, Tensor second_order, SymInt metadata_id, bool shared) -> Tensor",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "forward_into"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor info, Tensor coefficients, "
+        "Tensor first_order, Tensor second_order, SymInt metadata_id, bool shared, "
+        "Tensor(a9!) result) -> ()",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "backward"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor grad_output, Tensor info, "
+        "Tensor coefficients, Tensor first_order, Tensor second_order, SymInt metadata_id, "
+        "bool shared, SymInt needed=7) -> (Tensor, Tensor, Tensor)",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "backward_into"):
+        "(Tensor left, Tensor right, Tensor weight, Tensor grad_output, Tensor info, "
+        "Tensor coefficients, Tensor first_order, Tensor second_order, SymInt metadata_id, "
+        "bool shared, SymInt needed, Tensor(a11!) gx, Tensor(a12!) gy, Tensor(a13!) gw) -> ()",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "radial_stream_forward"):
+        "(Tensor left, Tensor angular, Tensor radial, Tensor alpha, Tensor bias, Tensor info, "
+        "Tensor coefficients, Tensor first_order, Tensor second_order, SymInt metadata_id, "
+        "bool has_bias, bool save_first) -> (Tensor, Tensor)",
+    ("ictc_o2_hp_v0_1_6_dev0_uvu", "radial_stream_backward"):
+        "(Tensor left, Tensor angular, Tensor radial, Tensor alpha, Tensor bias, "
+        "Tensor cached_weights, Tensor grad_output, Tensor info, Tensor coefficients, "
+        "Tensor first_order, Tensor second_order, SymInt metadata_id, bool has_bias, "
+        "SymInt needed=31) -> (Tensor, Tensor, Tensor, Tensor, Tensor)",
+}
+
+
+@pytest.mark.parametrize("namespace,name", sorted(_REFERENCE_SCHEMAS))
+def test_ops_resolve_under_reference_namespaces(namespace, name):
+    """Callers and compiled graphs name the reference's versioned ops."""
+    import ictc_o2_hp
+    from ictc_o2_hp import ops, radial_ops, uvu_ops  # noqa: F401  (registration)
+    assert ictc_o2_hp.__version__.replace(".", "_") == "0_1_6_dev0"
+    op = getattr(getattr(torch.ops, namespace), name).default
+    schema = str(op._schema)
+    assert schema == f"{namespace}::{name}{_REFERENCE_SCHEMAS[(namespace, name)]}"
