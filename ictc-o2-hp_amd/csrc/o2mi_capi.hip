@@ -124,6 +124,32 @@ __global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ out, int6
   if (i < n) out[i] = v;
 }
 
+// Scratch of the allocation-free backward (o2mi_tp_backward_noalloc_f32): the
+// dw partial rows and the reduction's second stage.  Every GPU the library
+// runs on holds its own copy until the process ends.  In host code the name
+// is only a stand-in: kernels get the address from scratch_address().
+static __device__ __align__(256) float scratch[O2MI_TP_SCRATCH_BYTES / sizeof(float)];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with hipGetSymbolAddress.
+int scratch_address(float** out) {
+  static std::mutex mu;
+  static float* address[64] = {};
+  int device = 0;
+  const hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail_hip(err, "hipGetDevice");
+  if (device < 0 || device >= 64) return fail(O2MI_ERR_INVALID_ARGUMENT, "device index above 63");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!address[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+    address[device] = static_cast<float*>(p);
+  }
+  *out = address[device];
+  return O2MI_OK;
+}
+
 struct DeviceInfo {
   int cus = 0;
 };
@@ -199,11 +225,10 @@ struct BackwardShape {
   size_t bytes;
 };
 
-BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant) {
+BackwardShape backward_shape_for(const o2mi_tp_plan* p, int64_t n_rows, int variant,
+                                 int64_t target) {
   BackwardShape s{};
   s.variant = variant;
-  const int64_t target =
-      (int64_t)p->set->blocks_per_cu(variant, true) * device_cus() * O2MI_BWD_BLOCKS_MULT;
   s.geom = geometry(p, n_rows, target, o2mi::kBackwardTile, &s.grid);
   s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
   s.splits = s.partial_rows <= kReduceSplitRows
@@ -212,6 +237,33 @@ BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant)
   const int64_t floats = (s.partial_rows + (s.splits > 1 ? s.splits : 0)) * p->weight_numel;
   s.bytes = n_rows > 0 ? (size_t)floats * sizeof(float) : 0;
   return s;
+}
+
+// The occupancy-sized grid; with `max_bytes` set, the largest grid (fewest
+// row groups removed) whose partial rows fit in max_bytes.  A shape that does
+// not fit even with one row group comes back with bytes > max_bytes.
+BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant,
+                             size_t max_bytes = SIZE_MAX) {
+  const int64_t target =
+      (int64_t)p->set->blocks_per_cu(variant, true) * device_cus() * O2MI_BWD_BLOCKS_MULT;
+  BackwardShape s = backward_shape_for(p, n_rows, variant, target);
+  if (s.bytes <= max_bytes) return s;
+  // Bytes grow with the number of row groups: bisect on it.
+  const int64_t tiles = s.geom.tiles;
+  int64_t lo = 1, hi = s.grid / tiles;  // lo may not fit; hi does not
+  BackwardShape best = backward_shape_for(p, n_rows, variant, tiles);
+  if (best.bytes > max_bytes) return best;
+  while (hi - lo > 1) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    BackwardShape t = backward_shape_for(p, n_rows, variant, mid * tiles);
+    if (t.bytes <= max_bytes) {
+      lo = mid;
+      best = t;
+    } else {
+      hi = mid;
+    }
+  }
+  return best;
 }
 
 hipError_t fill(float* out, int64_t n, float v, hipStream_t stream) {
@@ -228,6 +280,59 @@ hipError_t column_sum(const float* in, int64_t nrows, int64_t ncols, int64_t spl
   hipLaunchKernelGGL(column_sum_kernel, grid, dim3(256), 0, stream, in, nrows, ncols, per_split,
                      out);
   return hipGetLastError();
+}
+
+// Shared body of the backward entry points.  `fit_grid`: shrink the grid so
+// that the partial rows fit in `workspace_bytes` instead of failing.
+int tp_backward(const o2mi_tp_plan* plan, const float* x, const float* y, const float* w,
+                const float* g, float* dx, float* dy, float* dw, float* workspace,
+                size_t workspace_bytes, bool fit_grid, int64_t n_rows, int needed,
+                void* stream) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
+  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
+  if ((needed & 4) && !dw) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL dw for a requested gradient");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_rows == 0 || needed == 0) {
+    // Empty inputs: dx and dy are empty (their pointers may be NULL), dw = 0.
+    if (needed & 4) {
+      const hipError_t err = fill(dw, plan->weight_numel, 0.f, s);
+      if (err != hipSuccess) return fail_hip(err, "dw fill");
+    }
+    return O2MI_OK;
+  }
+  if (!x || !y || !w || !g) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
+  if (((needed & 1) && !dx) || ((needed & 2) && !dy))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
+  if (n_rows > (int64_t)INT32_MAX * 64)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  const int variant = pick_variant(plan, {x, y, g, (needed & 1) ? dx : nullptr,
+                                          (needed & 2) ? dy : nullptr});
+  const bool fit = fit_grid && (needed & 4);
+  const BackwardShape shape = backward_shape(plan, n_rows, variant, fit ? workspace_bytes : SIZE_MAX);
+  if (fit && shape.bytes > workspace_bytes)
+    return fail(O2MI_ERR_WORKSPACE, "weight_numel too large for the backward scratch");
+  if ((needed & 4) && (!workspace || workspace_bytes < shape.bytes))
+    return fail(O2MI_ERR_WORKSPACE, "workspace smaller than o2mi_tp_backward_workspace_bytes");
+  float* partial = workspace;
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_BACKWARD);
+  hipError_t err = plan->set->backward(variant, x, y, w, g, dx, dy, partial, shape.geom,
+                                       shape.grid, needed, s);
+  if (timing) o2mi_timing_end(s, &timed);
+  if (err != hipSuccess) return fail_hip(err, "tp backward launch");
+  if (needed & 4) {
+    const int64_t pw = plan->weight_numel;
+    if (shape.splits == 1) {
+      err = column_sum(partial, shape.partial_rows, pw, 1, dw, s);
+    } else {
+      float* second = partial + shape.partial_rows * pw;
+      err = column_sum(partial, shape.partial_rows, pw, shape.splits, second, s);
+      if (err == hipSuccess) err = column_sum(second, shape.splits, pw, 1, dw, s);
+    }
+    if (err != hipSuccess) return fail_hip(err, "dw reduction launch");
+  }
+  return O2MI_OK;
 }
 
 }  // namespace
@@ -424,48 +529,23 @@ size_t o2mi_tp_backward_workspace_bytes(const o2mi_tp_plan* plan, int64_t n_rows
 int o2mi_tp_backward_f32(const o2mi_tp_plan* plan, const float* x, const float* y, const float* w,
                          const float* g, float* dx, float* dy, float* dw, void* workspace,
                          size_t workspace_bytes, int64_t n_rows, int needed, void* stream) {
-  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
-  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
-  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
-  if ((needed & 4) && !dw) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL dw for a requested gradient");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n_rows == 0 || needed == 0) {
-    // Empty inputs: dx and dy are empty (their pointers may be NULL), dw = 0.
-    if (needed & 4) {
-      const hipError_t err = fill(dw, plan->weight_numel, 0.f, s);
-      if (err != hipSuccess) return fail_hip(err, "dw fill");
-    }
-    return O2MI_OK;
+  return tp_backward(plan, x, y, w, g, dx, dy, dw, static_cast<float*>(workspace),
+                     workspace_bytes, false, n_rows, needed, stream);
+}
+
+int o2mi_tp_backward_noalloc_f32(const o2mi_tp_plan* plan, const float* x, const float* y,
+                                 const float* w, const float* g, float* dx, float* dy, float* dw,
+                                 int64_t n_rows, int needed, void* stream) {
+  float* partial = nullptr;
+  // Only the weight adjoint uses the scratch.  Its partial rows and second
+  // stage are written in full before they are read, so nothing needs to be
+  // cleared between calls.
+  if ((needed & 4) && n_rows > 0) {
+    const int status = scratch_address(&partial);
+    if (status != O2MI_OK) return status;
   }
-  if (!x || !y || !w || !g) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
-  if (((needed & 1) && !dx) || ((needed & 2) && !dy))
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
-  if (n_rows > (int64_t)INT32_MAX * 64)
-    return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
-  const int variant = pick_variant(plan, {x, y, g, (needed & 1) ? dx : nullptr,
-                                          (needed & 2) ? dy : nullptr});
-  const BackwardShape shape = backward_shape(plan, n_rows, variant);
-  if ((needed & 4) && (!workspace || workspace_bytes < shape.bytes))
-    return fail(O2MI_ERR_WORKSPACE, "workspace smaller than o2mi_tp_backward_workspace_bytes");
-  float* partial = static_cast<float*>(workspace);
-  O2miTimed timed;
-  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_BACKWARD);
-  hipError_t err = plan->set->backward(variant, x, y, w, g, dx, dy, partial, shape.geom,
-                                       shape.grid, needed, s);
-  if (timing) o2mi_timing_end(s, &timed);
-  if (err != hipSuccess) return fail_hip(err, "tp backward launch");
-  if (needed & 4) {
-    const int64_t pw = plan->weight_numel;
-    if (shape.splits == 1) {
-      err = column_sum(partial, shape.partial_rows, pw, 1, dw, s);
-    } else {
-      float* second = partial + shape.partial_rows * pw;
-      err = column_sum(partial, shape.partial_rows, pw, shape.splits, second, s);
-      if (err == hipSuccess) err = column_sum(second, shape.splits, pw, 1, dw, s);
-    }
-    if (err != hipSuccess) return fail_hip(err, "dw reduction launch");
-  }
-  return O2MI_OK;
+  return tp_backward(plan, x, y, w, g, dx, dy, dw, partial, O2MI_TP_SCRATCH_BYTES, true, n_rows,
+                     needed, stream);
 }
 
 }  // extern "C"

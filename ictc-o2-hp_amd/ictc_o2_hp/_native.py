@@ -63,6 +63,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_tp_backward_workspace_bytes.argtypes = [vp, c_i64]
     lib.o2mi_tp_backward_f32.restype = c_int
     lib.o2mi_tp_backward_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, vp, c_sz, c_i64, c_int, vp]
+    lib.o2mi_tp_backward_noalloc_f32.restype = c_int
+    lib.o2mi_tp_backward_noalloc_f32.argtypes = [vp, fp, fp, fp, fp, fp, fp, fp, c_i64, c_int, vp]
     prob = ctypes.POINTER(UvuProblem)
     lib.o2mi_uvu_forward_f32.restype = c_int
     lib.o2mi_uvu_forward_f32.argtypes = [prob, fp, fp, fp, fp, vp]

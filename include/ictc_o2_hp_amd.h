@@ -96,6 +96,26 @@ int o2mi_tp_backward_f32(const o2mi_tp_plan *plan, const float *x, const float *
                          float *dw, void *workspace, size_t workspace_bytes,
                          int64_t n_rows, int needed, void *stream);
 
+/* Bytes of the library-owned device scratch of o2mi_tp_backward_noalloc_f32
+ * (one array per GPU, held until the process ends). */
+#define O2MI_TP_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* o2mi_tp_backward_f32 without a workspace argument and without any device
+ * allocation: the dw partial rows live in a library-owned device array of
+ * O2MI_TP_SCRATCH_BYTES per GPU.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Results equal
+ * o2mi_tp_backward_f32's (bitwise whenever that call's workspace would fit in
+ * the scratch; otherwise the grid is reduced to fit and dw is a different
+ * fixed-order sum, equal within fp32 rounding).  Returns O2MI_ERR_WORKSPACE
+ * when even one block's partial rows exceed the scratch (weight_numel too
+ * large).  Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (several streams or threads) race and must be serialised by the
+ * caller. */
+int o2mi_tp_backward_noalloc_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
+                                 const float *w, const float *g, float *dx, float *dy,
+                                 float *dw, int64_t n_rows, int needed, void *stream);
+
 /* ---- uvu product (UvuTensorProduct) ---------------------------------------
  * One problem description per call; the tables are device arrays the caller
  * owns (the module buffers _path_info, _coefficients, _first_order,
