@@ -77,13 +77,41 @@ def _args():
     return p.parse_args()
 
 
+def _cpu_threads():
+    """Host threads for the CPU baseline: every core in this process's affinity
+    mask, bounded by OMP_NUM_THREADS when the host declares its CPU share there
+    (the GPU boxes give one GPU's job 16 cores of a larger mask)."""
+    cores = len(os.sched_getaffinity(0))
+    declared = os.environ.get("OMP_NUM_THREADS", "")
+    if declared.isdigit() and int(declared) > 0:
+        cores = min(cores, int(declared))
+    return cores
+
+
+def _one_piece(port, rows, seed):
+    """Seconds of one fp32 forward + autograd VJP over `rows` rows in one piece."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    width = port.plan.width
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    y = rng.standard_normal((rows, width)).astype(np.float32)
+    w = (rng.standard_normal(port.plan.weight_numel) * 0.02).astype(np.float32)
+    g = np.ones((rows, width), dtype=np.float32)
+    port.forward_vjp(x[:64], y[:64], w, g[:64])         # warm-up
+    start = time.perf_counter()
+    port.forward_vjp(x, y, w, g)
+    return time.perf_counter() - start
+
+
 def _cpu_baseline(channels, m_max, parity, width, budget_s):
-    """Reference CPU algebra (fp32, autograd) on 2048-row chunks of the workload."""
+    """Reference CPU algebra (fp32, autograd) on 2048-row chunks of the workload,
+    plus BASELINE.json configs[0] (C32 m2 canonical, N=4096) and configs[1]
+    (C128 m6 full, N=6400) each timed in one piece."""
     import numpy as np
     import torch
     from oracle.cpu_port import CPUPort
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     port = CPUPort(channels, m_max, parity)
     rng = np.random.default_rng(0)
@@ -100,10 +128,17 @@ def _cpu_baseline(channels, m_max, parity, width, budget_s):
         elapsed = time.perf_counter() - start
         if elapsed >= budget_s:
             break
+    pieces = {}
+    for name, (c, m, par, n) in (("configs0", (32, 2, "canonical", 4096)),
+                                 ("configs1", (128, 6, "full", 6400))):
+        seconds = _one_piece(CPUPort(c, m, par), n, 1)
+        pieces[name] = {"rows": n, "ms": seconds * 1e3, "rows_per_s": n / seconds,
+                        "workload": f"C{c} m{m} {par}, fp32 forward + autograd dx/dy/dw"}
     return {"value": rows / elapsed, "unit": "rows/s", "cores": cores, "kind": "port",
-            "cpu": _cpu_model(),
+            "cpu": _cpu_model(), "affinity_cores": len(os.sched_getaffinity(0)),
             "sample": f"{rows} rows in {chunk}-row chunks of C{channels} m{m_max} {parity}, "
-                      f"fp32 forward + autograd dx/dy/dw, {elapsed:.1f} s"}
+                      f"fp32 forward + autograd dx/dy/dw, {elapsed:.1f} s",
+            "one_piece": pieces}
 
 
 def _cpu_model():
@@ -152,27 +187,54 @@ def _traffic(path: Path, key: str):
 
 
 def _timed_steps(torch, step, steps, warmup):
-    """Warm up, then time `steps` steps with events on torch's current stream
-    (the stream every kernel of the step is launched on)."""
+    """Warm up, then three passes of `steps` steps on torch's current stream
+    (the stream every kernel of the step is launched on), each bracketed by
+    synchronizes:
+
+    1. the timed region of ``value``: one HIP event pair around all steps and
+       nothing between the steps;
+    2. one event after every step, for the per-step median and IQR;
+    3. the library's per-kernel HIP event pairs (o2mi_kernel_timing) around
+       every main kernel, for the kernel durations behind ``roofline``.
+
+    Each recorded event puts a few microseconds between the launches around
+    it, so the per-step and per-kernel events are kept out of pass 1.
+    Returns (ms per step of pass 1, wall ms per step of pass 1, per-kernel
+    records of pass 3, per-step samples of pass 2)."""
     from ictc_o2_hp import _native
     for _ in range(max(1, warmup)):
         step()
     torch.cuda.synchronize()
     _native.kernel_timing_read_kinds()          # drop warm-up records
-    _native.kernel_timing(True)
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms_per_step = start.elapsed_time(stop) / steps
+
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
     events[0].record()
     for i in range(steps):
         step()
         events[i + 1].record()
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
+    samples = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+
+    _native.kernel_timing(True)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
     _native.kernel_timing(False)
     kinds = _native.kernel_timing_read_kinds()
-    samples = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
-    return events[0].elapsed_time(events[-1]) / steps, wall_ms / steps, kinds, samples
+    return ms_per_step, wall_ms / steps, kinds, samples
 
 
 def _radial_chain(torch, device, edges, nodes=65536, channels=64, m_max=4, hidden=64,
@@ -224,7 +286,7 @@ def _radial_cpu_baseline(channels, m_max, hidden, budget_s):
     import numpy as np
     from oracle import uvu_oracle as U
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = _cpu_threads()
     plan = U.UvuOraclePlan(channels, 1, m_max, parity="canonical")
     rng = np.random.default_rng(0)
     chunk = 512
