@@ -1,5 +1,6 @@
-"""Public operators with the internal Cartesian O(2) coefficient source
-(``api.py`` of Parity-LRX/ICTC-O2-HP: same names, arguments and errors)."""
+"""The public TensorProduct classes, with the package's own O(2) coupling
+tables (``api.py`` of Parity-LRX/ICTC-O2-HP: same names, arguments and
+errors)."""
 from __future__ import annotations
 
 from . import o2_math
@@ -15,12 +16,13 @@ def _validate(channels, m_max):
 
 
 class TensorProduct(FlatPathWeightedTensorProductO2):
-    """Flat channel-major O(2) product with all path weights trainable.
+    """O(2) tensor product on flat rows ``(*batch, representation_dimension)``,
+    one trainable weight per (path, output channel) in ``weight``.
 
-    Inputs/outputs: ``(*batch, representation_dimension)``.  Positive-frequency
-    blocks use ``[copy, channel, component]`` in full parity and
-    ``[channel, component]`` in canonical parity; the second copy keeps its
-    reflection-twisted Cartesian basis.
+    Row layout: the scalar blocks, then per frequency m a block stored
+    channel-major, ``[copy, channel, component]`` (full parity, two copies)
+    or ``[channel, component]`` (canonical).  Copy 1 is stored in its own
+    Cartesian basis, a quarter turn J away from copy 0's.
     """
 
     def __init__(self, channels, m_max, *, parity="full", normalization="component"):
@@ -30,7 +32,8 @@ class TensorProduct(FlatPathWeightedTensorProductO2):
 
 
 class TupleTensorProduct(PackedPathWeightedTensorProductO2):
-    """One ``(*batch, multiplicity, irrep_dimension)`` tensor per block."""
+    """Tuple form: inputs and output are one tensor per block, shaped
+    ``(*batch, multiplicity, irrep_dimension)``; same weights as TensorProduct."""
 
     def __init__(self, channels, m_max, *, parity="full", normalization="component"):
         _validate(channels, m_max)
@@ -39,8 +42,10 @@ class TupleTensorProduct(PackedPathWeightedTensorProductO2):
 
 
 class ComponentMajorTensorProduct(ComponentMajorPathWeightedTensorProductO2):
-    """Flat product with ``[copy, component, channel]`` frequency blocks; the
-    bases are the same as TensorProduct's."""
+    """TensorProduct with component-major frequency blocks:
+    ``[copy, component, channel]`` (full) or ``[component, channel]``
+    (canonical).  Only the storage order differs; values and copy bases are
+    TensorProduct's."""
 
     def __init__(self, channels, m_max, *, parity="full", normalization="component"):
         _validate(channels, m_max)

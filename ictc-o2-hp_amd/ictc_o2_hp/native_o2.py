@@ -2,8 +2,8 @@
 
 Module surface of Parity-LRX/ICTC-O2-HP:
 
-* ``FullParityPathWeightedTensorProductO2``: one parameter per path, the
-  original einsum algebra (``native_o2.py:64-221``);
+* ``FullParityPathWeightedTensorProductO2``: one parameter per path
+  (``native_o2.py:64-221``), evaluated with the flat-row PyTorch algebra;
 * ``PackedPathWeightedTensorProductO2``: the same paths with one flat
   ``weight`` and ``copy_weights_to_r5`` / ``load_weights_from_r5``
   (``fast_o2.py:152-186``);
@@ -12,7 +12,7 @@ Module surface of Parity-LRX/ICTC-O2-HP:
 
 State-dict keys and shapes match the reference: ``weight`` (or
 ``weights.<p>``), ``cg_<p>`` and ``odd_to_even`` / ``even_to_odd`` persistent;
-routing and kernel metadata non-persistent.  CUDA float32 inputs on the
+kernel metadata non-persistent.  CUDA float32 inputs on the
 weight's device run the gfx950 kernels; other devices and dtypes run the
 PyTorch algebra, as in the reference (``triton_o2.py:1134-1143``).
 """
@@ -54,21 +54,11 @@ class FullParityPathWeightedTensorProductO2(torch.nn.Module):
         self.paths = self._plan.paths
 
         self.weights = torch.nn.ParameterList()
-        self._cg_names, self._index_names = [], []
-        for p, (key1, key2, key3) in enumerate(self.paths):
-            out_mul = self.block_by_key[key3].multiplicity
-            in1 = self.block_by_key[key1].multiplicity
-            in2 = self.block_by_key[key2].multiplicity
+        for p, path in enumerate(self._plan.table):
             # Same draw order as the reference: one randn(out_mul) per path.
-            self.weights.append(torch.nn.Parameter(torch.randn(out_mul) * 0.02))
+            self.weights.append(torch.nn.Parameter(torch.randn(path.weight_count) * 0.02))
             self.register_buffer(f"cg_{p}", torch.from_numpy(self._plan.cg[p].copy()),
                                  persistent=True)
-            self.register_buffer(f"input1_index_{p}", torch.arange(out_mul) % in1,
-                                 persistent=False)
-            self.register_buffer(f"input2_index_{p}", torch.arange(out_mul) % in2,
-                                 persistent=False)
-            self._cg_names.append(f"cg_{p}")
-            self._index_names.append((f"input1_index_{p}", f"input2_index_{p}"))
         j = torch.tensor(_J, dtype=torch.float64)
         self.register_buffer("odd_to_even", j.transpose(0, 1).contiguous(), persistent=True)
         self.register_buffer("even_to_odd", j.contiguous(), persistent=True)
@@ -82,48 +72,42 @@ class FullParityPathWeightedTensorProductO2(torch.nn.Module):
         return sum(p.numel() for p in self.parameters())
 
     def representation_spec(self):
-        rows = []
-        for b in self.blocks:
-            if b.frequency == 0:
-                labels = b.token
-            else:
-                labels = str(b.frequency) if self.parity == "canonical" else \
-                    f"{b.frequency}e+{b.frequency}o"
-            rows.append({"labels": labels, "frequency": b.frequency,
-                         "irrep_dimension": b.irrep_dimension,
-                         "multiplicity": b.multiplicity, "parity_copies": b.parity_copies})
-        return rows
+        """One dict per block (``native_o2.py:145-165``): its label ("0e", "0o",
+        "m" canonical, "me+mo" full), frequency, irrep dimension, multiplicity
+        and parity copies."""
+        fields = ("frequency", "irrep_dimension", "multiplicity", "parity_copies")
+        spec = []
+        for block in self.blocks:
+            m = block.frequency
+            label = block.token if m == 0 else (f"{m}e+{m}o" if self.parity == "full" else str(m))
+            spec.append({"labels": label, **{name: getattr(block, name) for name in fields}})
+        return spec
 
-    def _twist(self, key, value, matrix):
-        if key[0] != "freq" or self.parity == "canonical":
-            return value
-        even, odd = value.split(self.channels, dim=-2)
-        t = matrix.to(device=value.device, dtype=value.dtype)
-        return torch.cat((even, torch.einsum("...ci,ij->...cj", odd, t)), dim=-2)
+    def _packed_weight(self) -> torch.Tensor:
+        """All path weights in path order, as one differentiable vector."""
+        return torch.cat(list(self.weights))
 
     def forward(self, left, right):
-        """Original einsum algebra (``native_o2.py:183-221``)."""
+        """Tuple API: one (*batch, multiplicity, irrep_dimension) tensor per
+        block in and out (``native_o2.py:183-221``), evaluated as the flat-row
+        algebra on the concatenated blocks in ``internal_compute_dtype``."""
         if len(left) != len(self.keys) or len(right) != len(self.keys):
             raise ValueError("one tensor per representation block is required")
-        lhs = {k: self._twist(k, v, self.odd_to_even) for k, v in zip(self.keys, left)}
-        rhs = {k: self._twist(k, v, self.odd_to_even) for k, v in zip(self.keys, right)}
-        sample = left[0]
-        out = {b.key: torch.zeros(*sample.shape[:-2], b.multiplicity, b.irrep_dimension,
-                                  dtype=sample.dtype, device=sample.device)
-               for b in self.blocks}
+        batch = left[0].shape[:-2]
         dtype = self.internal_compute_dtype
-        for p, (key1, key2, key3) in enumerate(self.paths):
-            i1, i2 = (getattr(self, n) for n in self._index_names[p])
-            a = lhs[key1].index_select(-2, i1).to(dtype)
-            b = rhs[key2].index_select(-2, i2).to(dtype)
-            cg = getattr(self, self._cg_names[p]).to(device=sample.device, dtype=dtype)
-            value = torch.einsum("...om,...on,mnk,o->...ok", a, b, cg,
-                                 self._path_weight(p).to(dtype))
-            out[key3] = out[key3] + value.to(sample.dtype)
-        return tuple(self._twist(k, out[k], self.even_to_odd) for k in self.keys)
+        width = self.representation_dimension
+        x = torch.cat([v.reshape(*batch, -1) for v in left], dim=-1).reshape(-1, width)
+        y = torch.cat([v.reshape(*batch, -1) for v in right], dim=-1).reshape(-1, width)
+        out = flat_forward(x.to(dtype), y.to(dtype), self._packed_weight().to(dtype), self._plan)
+        out = out.to(left[0].dtype).reshape(*batch, width)
+        return _split_blocks(out, self._plan)
 
-    def _path_weight(self, p: int) -> torch.Tensor:
-        return self.weights[p]
+
+def _split_blocks(flat: torch.Tensor, plan: TPPlan):
+    """Channel-major flat rows [..., W] -> one [..., multiplicity, dim] view per block."""
+    sizes = [b.multiplicity * b.irrep_dimension for b in plan.blocks]
+    return tuple(part.unflatten(-1, (b.multiplicity, b.irrep_dimension))
+                 for part, b in zip(flat.split(sizes, dim=-1), plan.blocks))
 
 
 def _path_metadata(plan: TPPlan, layout: int):
@@ -160,9 +144,8 @@ class PackedPathWeightedTensorProductO2(FullParityPathWeightedTensorProductO2):
         self.register_buffer("_weight_path_coefficients", coefficients, persistent=False)
         self._metadata_id = ops.register(self._plan, self._layout)
 
-    def _path_weight(self, p: int) -> torch.Tensor:
-        start, end = self._weight_offsets[p]
-        return self.weight[start:end]
+    def _packed_weight(self) -> torch.Tensor:
+        return self.weight
 
     def copy_weights_to_r5(self, reference: FullParityPathWeightedTensorProductO2) -> None:
         """Copy the packed weight into a per-path reference module (``fast_o2.py:173-178``)."""
@@ -201,10 +184,6 @@ class PackedPathWeightedTensorProductO2(FullParityPathWeightedTensorProductO2):
                            self.weight.to(dtype), self._plan, self._layout)
         return out.to(left.dtype).reshape(left.shape)
 
-    def _block_slices(self):
-        for start, block in zip(self._plan.key_offsets, self.blocks):
-            yield start, block.multiplicity * block.irrep_dimension, block
-
     def forward(self, left, right):
         """Tuple API: one (*batch, multiplicity, irrep_dimension) tensor per block."""
         if len(left) != len(self.keys) or len(right) != len(self.keys):
@@ -212,9 +191,7 @@ class PackedPathWeightedTensorProductO2(FullParityPathWeightedTensorProductO2):
         batch = left[0].shape[:-2]
         lf = torch.cat([v.reshape(*batch, -1) for v in left], dim=-1)
         rf = torch.cat([v.reshape(*batch, -1) for v in right], dim=-1)
-        out = self._flat(lf, rf)
-        return tuple(out[..., s:s + n].reshape(*batch, b.multiplicity, b.irrep_dimension)
-                     for s, n, b in self._block_slices())
+        return _split_blocks(self._flat(lf, rf), self._plan)
 
 
 class FlatPathWeightedTensorProductO2(PackedPathWeightedTensorProductO2):
@@ -236,36 +213,32 @@ class ComponentMajorPathWeightedTensorProductO2(PackedPathWeightedTensorProductO
         self._layout = 1 if parity == "canonical" else 2
         super().__init__(*args, **kwargs)
 
+    def _channel_major_columns(self, device) -> torch.Tensor:
+        """Column of this layout's row that holds each channel-major element:
+        channel_major_row = row[..., columns] (``triton_o2.py:110-121``)."""
+        columns = getattr(self, "_columns", None)
+        if columns is None:
+            plan = self._plan
+            order = [plan.element_offset(key, channel, component, self._layout)
+                     for key, block in enumerate(plan.blocks)
+                     for channel in range(block.multiplicity)
+                     for component in range(block.irrep_dimension)]
+            columns = torch.tensor(order, dtype=torch.long)
+            self._columns = columns
+            self._inverse_columns = torch.argsort(columns)
+        return columns.to(device)
+
     def _unpack(self, value: torch.Tensor):
-        batch = value.shape[:-1]
-        pieces = []
-        for start, width, block in self._block_slices():
-            part = value[..., start:start + width]
-            mul, dim = block.multiplicity, block.irrep_dimension
-            if dim == 1:
-                part = part.reshape(*batch, mul, 1)
-            elif self.parity == "full":
-                part = part.reshape(*batch, mul // self.channels, dim, self.channels) \
-                    .transpose(-1, -2).reshape(*batch, mul, dim)
-            else:
-                part = part.reshape(*batch, dim, mul).transpose(-1, -2)
-            pieces.append(part)
-        return tuple(pieces)
+        """Component-major rows [..., W] -> one [..., multiplicity, dim] tensor per block."""
+        columns = self._channel_major_columns(value.device)
+        return _split_blocks(value.index_select(-1, columns), self._plan)
 
     def _pack(self, blocks) -> torch.Tensor:
-        pieces = []
-        for value, block in zip(blocks, self.blocks):
-            batch = value.shape[:-2]
-            width = block.multiplicity * block.irrep_dimension
-            if block.irrep_dimension == 1:
-                part = value.reshape(*batch, width)
-            elif self.parity == "full":
-                part = value.reshape(*batch, block.parity_copies, self.channels,
-                                     block.irrep_dimension).transpose(-1, -2).reshape(*batch, width)
-            else:
-                part = value.transpose(-1, -2).reshape(*batch, width)
-            pieces.append(part)
-        return torch.cat(pieces, dim=-1)
+        """Inverse of ``_unpack``."""
+        batch = blocks[0].shape[:-2]
+        flat = torch.cat([b.reshape(*batch, -1) for b in blocks], dim=-1)
+        self._channel_major_columns(flat.device)
+        return flat.index_select(-1, self._inverse_columns.to(flat.device))
 
     def forward(self, left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
         if (left.ndim < 1 or left.shape[-1] != self.representation_dimension
@@ -276,18 +249,21 @@ class ComponentMajorPathWeightedTensorProductO2(PackedPathWeightedTensorProductO
 
 def apply_full_parity_o2(module, tensors: Iterable[torch.Tensor],
                          group_element: torch.Tensor):
-    """Act with an O(2) element on per-block tensors in the public copy bases
-    (``native_o2.py:224-247``): the second copy transforms with det(g) * R_m(g)."""
-    outputs = []
+    """Act with the O(2) element ``group_element`` [..., 2, 2] on per-block
+    tensors [..., multiplicity, dim] in the public copy bases
+    (``native_o2.py:224-247``): every row of a block transforms with the key's
+    representation matrix, and in full parity the second copy of each frequency
+    block (its last C rows) carries an extra factor det(g)."""
     det = torch.linalg.det(group_element)
+    outputs = []
     for block, value in zip(module.blocks, tensors):
         matrix = module.o2.o2_representation(group_element, block.key).to(
             device=value.device, dtype=value.dtype)
-        if block.frequency == 0 or module.parity == "canonical":
-            outputs.append(torch.einsum("...ab,...cb->...ca", matrix, value))
-            continue
-        even, odd = value.split(module.channels, dim=-2)
-        odd_matrix = det[..., None, None] * matrix
-        outputs.append(torch.cat((torch.einsum("...ab,...cb->...ca", matrix, even),
-                                  torch.einsum("...ab,...cb->...ca", odd_matrix, odd)), dim=-2))
+        moved = torch.matmul(value, matrix.transpose(-1, -2))
+        if module.parity == "full" and block.frequency > 0:
+            second_copy = torch.arange(block.multiplicity, device=value.device) >= module.channels
+            scale = torch.where(second_copy, det.to(value.dtype)[..., None],
+                                torch.ones((), dtype=value.dtype, device=value.device))
+            moved = moved * scale[..., None]
+        outputs.append(moved)
     return tuple(outputs)

@@ -1,5 +1,6 @@
-"""Pure PyTorch tuple operator with one parameter per path (``reference.py``
-of Parity-LRX/ICTC-O2-HP); it never touches the HIP library."""
+"""``ReferenceTensorProduct``: the tuple-API product with a separate
+parameter per path, evaluated in PyTorch only (``reference.py`` of
+Parity-LRX/ICTC-O2-HP); it never loads the HIP library."""
 from __future__ import annotations
 
 from . import o2_math
@@ -7,7 +8,7 @@ from .native_o2 import FullParityPathWeightedTensorProductO2
 
 
 class ReferenceTensorProduct(FullParityPathWeightedTensorProductO2):
-    """Original Cartesian path algebra, with one parameter per path."""
+    """Tuple-API O(2) product, weights ``weights.<p>`` per path, PyTorch only."""
 
     def __init__(self, channels, m_max, *, parity="full", normalization="component"):
         if int(channels) != channels or channels < 1:

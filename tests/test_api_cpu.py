@@ -213,3 +213,30 @@ def test_ops_resolve_under_reference_namespaces(namespace, name):
     op = getattr(getattr(torch.ops, namespace), name).default
     schema = str(op._schema)
     assert schema == f"{namespace}::{name}{_REFERENCE_SCHEMAS[(namespace, name)]}"
+
+
+@pytest.mark.parametrize("parity", ["canonical", "full"])
+def test_apply_full_parity_o2_is_a_symmetry_of_the_product(parity):
+    """f(g x, g y) = g f(x, y) for rotations and reflections, with g acting
+    through apply_full_parity_o2 in the public copy bases.  A missing det(g)
+    factor on copy 1 or a transposed representation matrix breaks it."""
+    from ictc_o2_hp import ReferenceTensorProduct
+    from ictc_o2_hp.native_o2 import apply_full_parity_o2
+    torch.manual_seed(9)
+    tp = ReferenceTensorProduct(3, 3, parity=parity).double()
+    tp.internal_compute_dtype = torch.float64
+    blocks = lambda: tuple(torch.randn(5, b.multiplicity, b.irrep_dimension, dtype=torch.float64)
+                           for b in tp.blocks)
+    x, y = blocks(), blocks()
+    for angle, reflect in ((0.7, False), (2.1, True)):
+        c, s = np.cos(angle), np.sin(angle)
+        g = torch.tensor([[c, -s], [s, c]], dtype=torch.float64)
+        if reflect:
+            g = g @ torch.tensor([[1.0, 0.0], [0.0, -1.0]], dtype=torch.float64)
+        lhs = tp(apply_full_parity_o2(tp, x, g), apply_full_parity_o2(tp, y, g))
+        rhs = apply_full_parity_o2(tp, tp(x, y), g)
+        for a, b in zip(lhs, rhs):
+            assert torch.allclose(a, b, atol=1e-12)
+    # The action of a reflection is not the identity on odd blocks.
+    moved = apply_full_parity_o2(tp, x, torch.diag(torch.tensor([1.0, -1.0], dtype=torch.float64)))
+    assert any(not torch.allclose(a, b) for a, b in zip(moved, x))
