@@ -240,3 +240,104 @@ def test_apply_full_parity_o2_is_a_symmetry_of_the_product(parity):
     # The action of a reflection is not the identity on odd blocks.
     moved = apply_full_parity_o2(tp, x, torch.diag(torch.tensor([1.0, -1.0], dtype=torch.float64)))
     assert any(not torch.allclose(a, b) for a, b in zip(moved, x))
+
+
+# ---- fixtures recorded from the reference (tests/golden/make_layouts_and_state.py)
+
+def _layout_cases():
+    data = np.load(GOLDEN / "layout_vectors.npz")
+    for name in sorted({k.split("/")[0] for k in data.files}):
+        c, m, parity, norm = name.split("_")
+        yield name, int(c[1:]), int(m[1:]), parity, norm, {k.split("/")[1]: data[k]
+                                                            for k in data.files
+                                                            if k.startswith(name + "/")}
+
+
+def test_oracle_component_major_layouts_match_reference_vectors():
+    """oracle layouts 1 / 2 (component-major) against the reference's
+    component-major product (triton_o2.py:1204-1278 CPU path, fp64)."""
+    for name, c, m, parity, norm, v in _layout_cases():
+        plan = O.OraclePlan(c, m, parity, norm)
+        layout = 1 if parity == "canonical" else 2
+        out = O.forward(plan, v["x"], v["y"], v["weight"], layout)
+        dx, dy, dw = O.backward(plan, v["x"], v["y"], v["weight"], v["g"], layout)
+        for ref, got in ((v["out"], out), (v["dx"], dx), (v["dy"], dy), (v["dw"], dw)):
+            assert O.normalized_error(ref, got) < 1e-12, name
+
+
+def test_component_major_module_matches_reference_vectors():
+    """ComponentMajorTensorProduct's CPU path in fp64 against the same vectors;
+    _unpack / _pack against the reference's storage order."""
+    from ictc_o2_hp import ComponentMajorTensorProduct, TensorProduct
+    for name, c, m, parity, norm, v in _layout_cases():
+        module = ComponentMajorTensorProduct(c, m, parity=parity, normalization=norm).double()
+        module.internal_compute_dtype = torch.float64
+        with torch.no_grad():
+            module.weight.copy_(torch.from_numpy(v["weight"]))
+        x = torch.from_numpy(v["x"]).requires_grad_()
+        y = torch.from_numpy(v["y"]).requires_grad_()
+        out = module(x, y)
+        grads = torch.autograd.grad(out, (x, y, module.weight), torch.from_numpy(v["g"]))
+        for ref, got in zip((v["out"], v["dx"], v["dy"], v["dw"]), (out, *grads)):
+            assert O.normalized_error(ref, got.detach().numpy()) < 1e-12, name
+        # Tuple round trip: the channel-major product on unpacked blocks, packed back.
+        flat = TensorProduct(c, m, parity=parity, normalization=norm).double()
+        flat.internal_compute_dtype = torch.float64
+        with torch.no_grad():
+            flat.weight.copy_(module.weight)
+        from ictc_o2_hp.native_o2 import _split_blocks
+        xb, yb = module._unpack(x.detach()), module._unpack(y.detach())
+        cat = lambda blocks: torch.cat([b.reshape(b.shape[0], -1) for b in blocks], dim=-1)
+        with torch.no_grad():
+            packed = module._pack(_split_blocks(flat(cat(xb), cat(yb)), flat._plan))
+        assert O.normalized_error(v["out"], packed.numpy()) < 1e-12, name
+
+
+_STATE_MODULES = {
+    "TensorProduct_c3_m2_full": lambda I: I.TensorProduct(3, 2, parity="full"),
+    "TensorProduct_c4_m3_canonical_norm": lambda I: I.TensorProduct(
+        4, 3, parity="canonical", normalization="norm"),
+    "TupleTensorProduct_c3_m2_full": lambda I: I.TupleTensorProduct(3, 2, parity="full"),
+    "ComponentMajorTensorProduct_c3_m2_canonical": lambda I: I.ComponentMajorTensorProduct(
+        3, 2, parity="canonical"),
+    "ReferenceTensorProduct_c3_m2_full": lambda I: I.ReferenceTensorProduct(3, 2, parity="full"),
+    "UvuTensorProduct_c3_v2_m2_full_shared": lambda I: I.UvuTensorProduct(3, 2, 2, parity="full"),
+    "UvuTensorProduct_c4_v1_m2_canonical_external": lambda I: I.UvuTensorProduct(
+        4, 1, 2, parity="canonical", shared_weights=False),
+    "ReferenceUvuTensorProduct_c2_v3_m1_full": lambda I: I.ReferenceUvuTensorProduct(
+        2, 3, 1, parity="full"),
+    "RadialUvuTensorProduct_c4_m2_canonical_h8": lambda I: I.RadialUvuTensorProduct(
+        I.UvuTensorProduct(4, 1, 2, parity="canonical", shared_weights=False),
+        torch.nn.Linear(8, I.UvuTensorProduct(4, 1, 2, parity="canonical",
+                                              shared_weights=False).weight_numel)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_STATE_MODULES))
+def test_state_dict_matches_reference_record(name):
+    """Keys, shapes and dtypes of every state-dict entry equal the reference's
+    (recorded from its modules), so checkpoints load strictly both ways."""
+    import json
+    import ictc_o2_hp
+    records = json.loads((GOLDEN / "state_dicts.json").read_text())
+    module = _STATE_MODULES[name](ictc_o2_hp)
+    mine = [[k, list(v.shape), str(v.dtype).replace("torch.", "")]
+            for k, v in module.state_dict().items()]
+    assert mine == records[name]
+
+
+@pytest.mark.parametrize("name", ["TensorProduct_c3_m2_full",
+                                  "ComponentMajorTensorProduct_c3_m2_canonical",
+                                  "UvuTensorProduct_c3_v2_m2_full_shared"])
+def test_reference_checkpoint_loads_and_reproduces_its_outputs(name):
+    import ictc_o2_hp
+    data = np.load(GOLDEN / "state_dict_values.npz")
+    prefix = f"{name}/state/"
+    state = {k[len(prefix):]: torch.from_numpy(data[k]) for k in data.files
+             if k.startswith(prefix)}
+    module = _STATE_MODULES[name](ictc_o2_hp)
+    module.load_state_dict(state, strict=True)
+    with torch.no_grad():
+        out = module(torch.from_numpy(data[f"{name}/x"]), torch.from_numpy(data[f"{name}/y"]))
+    assert O.normalized_error(data[f"{name}/out"].astype(np.float64),
+                              out.double().numpy()) < 1e-6

@@ -339,3 +339,21 @@ def test_headline_full_size_every_row_vs_fp64_algebra():
         del ref, ra, rb, a, b
     worst["dw"] = _normalized_error_t(dw64, dw)
     assert max(worst.values()) <= TOL, worst
+
+
+def test_component_major_matches_reference_layout_vectors():
+    """The component-major kernels (layouts 1 and 2) against the reference's
+    component-major product on its stored inputs (tests/golden/layout_vectors.npz)."""
+    from conftest import GOLDEN
+    from ictc_o2_hp import ComponentMajorTensorProduct
+    data = np.load(GOLDEN / "layout_vectors.npz")
+    for name in sorted({k.split("/")[0] for k in data.files}):
+        print(f"case component-major reference vectors {name}", flush=True)
+        c, m, parity, norm = name.split("_")
+        module = ComponentMajorTensorProduct(int(c[1:]), int(m[1:]), parity=parity,
+                                             normalization=norm).cuda()
+        with torch.no_grad():
+            module.weight.copy_(torch.from_numpy(data[f"{name}/weight"]).float())
+        got = _run(module, data[f"{name}/x"], data[f"{name}/y"], data[f"{name}/g"])
+        for key, value in zip(("out", "dx", "dy", "dw"), got):
+            assert O.normalized_error(data[f"{name}/{key}"], value) <= TOL, (name, key)
