@@ -80,6 +80,16 @@ def _check_inputs(*tensors: torch.Tensor) -> None:
             raise ValueError("o2 ops need contiguous tensors")
 
 
+def _check_shapes(op: str, native, left, right, weight, grad_output=None) -> None:
+    """The kernels read x, y (and the cotangent) as [N, W] rows and w as P_w
+    floats: anything else is refused before a launch."""
+    ok = (left.dim() == 2 and left.shape[1] == native.width and right.shape == left.shape
+          and weight.numel() == native.weight_numel
+          and (grad_output is None or grad_output.shape == left.shape))
+    if not ok:
+        raise ValueError(f"{op}: shapes do not match the plan")
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -88,11 +98,10 @@ def _stream(device: torch.device) -> int:
 def o2_forward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
                path_info: torch.Tensor, path_coefficients: torch.Tensor,
                metadata_id: int) -> torch.Tensor:
-    _check_inputs(left, right, weight)
     native = _native_plan(metadata_id)
-    n_rows, width = left.shape
-    if width != native.width or right.shape != left.shape or weight.numel() != native.weight_numel:
-        raise ValueError("o2_forward: shapes do not match the plan")
+    _check_shapes("o2_forward", native, left, right, weight)
+    _check_inputs(left, right, weight)
+    n_rows = left.shape[0]
     out = torch.empty_like(left)
     with torch.cuda.device(left.device):
         native.forward(left.data_ptr(), right.data_ptr(), weight.data_ptr(), out.data_ptr(),
@@ -111,11 +120,10 @@ def o2_backward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
                 path_coefficients: torch.Tensor,
                 metadata_id: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     grad_output = grad_output.contiguous()
-    _check_inputs(left, right, weight, grad_output)
     native = _native_plan(metadata_id)
-    n_rows, width = left.shape
-    if width != native.width or grad_output.shape != left.shape:
-        raise ValueError("o2_backward: shapes do not match the plan")
+    _check_shapes("o2_backward", native, left, right, weight, grad_output)
+    _check_inputs(left, right, weight, grad_output)
+    n_rows = left.shape[0]
     grad_left = torch.empty_like(left)
     grad_right = torch.empty_like(right)
     grad_weight = torch.empty_like(weight)

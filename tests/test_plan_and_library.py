@@ -119,3 +119,27 @@ def test_plan_create_validates_arguments(lib):
     assert (plan.width, plan.weight_numel) == (3328, 19712)
     plan = _native.TPNativePlan(5, 4, "canonical", "norm", 1)
     assert (plan.width, plan.weight_numel) == (45, 155)
+
+
+def test_tp_ops_refuse_mismatched_shapes_before_launch(lib):
+    """o2_forward / o2_backward check every operand's shape against the plan
+    (x, y, cotangent [N, W]; weight P_w) before any device work."""
+    import torch
+    from ictc_o2_hp import TensorProduct, ops
+    tp = TensorProduct(4, 2, parity="full")
+    w = tp.weight.detach()
+    x = torch.zeros(3, tp.representation_dimension)
+    meta = (tp._weight_path_info, tp._weight_path_coefficients, tp._metadata_id)
+    bad = [
+        (x, x[:2], w, x),                      # right rows differ
+        (x, x, w[:-1], x),                     # weight too short
+        (x, x, w, x[:, :-1]),                  # cotangent width
+        (x[:, :-1], x[:, :-1], w, x[:, :-1]),  # width not the plan's
+    ]
+    for left, right, weight, grad in bad:
+        with pytest.raises(ValueError, match="shapes do not match"):
+            ops.o2_backward(left, right, weight, grad, *meta)
+    with pytest.raises(ValueError, match="shapes do not match"):
+        ops.o2_forward(x, x[:2], w, *meta)
+    with pytest.raises(ValueError, match="shapes do not match"):
+        ops.o2_forward(x, x, w[:-1], *meta)
