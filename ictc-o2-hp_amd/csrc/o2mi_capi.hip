@@ -12,13 +12,14 @@
 
 #include "ictc_o2_hp_amd.h"
 #include "o2mi_error.hpp"
+#include "o2mi_tp_generic.hpp"
 #include "o2mi_tp_launch.hpp"
 
 // Defined by the generated registry (one entry per compiled plan).
 const o2mi::TPKernelSet* o2mi_find_tp_set(int m_max, int full, int normalization);
 
 struct o2mi_tp_plan {
-  const o2mi::TPKernelSet* set;
+  const o2mi::TPKernelSet* set;  // compiled kernels, or NULL (table-driven only)
   int channels;
   int m_max;
   int full;
@@ -26,6 +27,8 @@ struct o2mi_tp_plan {
   int layout;
   int64_t width;
   int64_t weight_numel;
+  int n_keys;
+  int n_paths;
 };
 
 std::string& o2mi_error_slot() {
@@ -282,6 +285,93 @@ hipError_t column_sum(const float* in, int64_t nrows, int64_t ncols, int64_t spl
   return hipGetLastError();
 }
 
+// Keys of TensorProduct(C, m_max, parity) in row order (0e, [0o], 1..M) as
+// (frequency, sign): scalars have frequency 0 and the parity sign.
+struct HostKey {
+  int m, sign;
+};
+
+std::vector<HostKey> host_keys(int m_max, bool full) {
+  std::vector<HostKey> keys{{0, 1}};
+  if (full) keys.push_back({0, -1});
+  for (int m = 1; m <= m_max; ++m) keys.push_back({m, 0});
+  return keys;
+}
+
+// Path count and packed weight count in units of C: every (k1, k2) and each
+// output key of their product present in the row (the selection rules of
+// o2_math.py:348-372), with mul(k3) weights per path.
+void count_paths(int m_max, bool full, int* n_paths, int64_t* units) {
+  const std::vector<HostKey> keys = host_keys(m_max, full);
+  const int freq_units = full ? 2 : 1;
+  *n_paths = 0;
+  *units = 0;
+  auto add = [&](HostKey k3) {
+    const bool present = k3.m == 0 ? (k3.sign == 1 || full) : k3.m <= m_max;
+    if (!present) return;
+    *n_paths += 1;
+    *units += k3.m == 0 ? 1 : freq_units;
+  };
+  for (const HostKey& a : keys) {
+    for (const HostKey& b : keys) {
+      if (a.m == 0 && b.m == 0) {
+        add({0, a.sign * b.sign});
+      } else if (a.m == 0 || b.m == 0) {
+        add({a.m == 0 ? b.m : a.m, 0});
+      } else if (a.m == b.m) {
+        add({0, 1});
+        add({0, -1});
+        add({2 * a.m, 0});
+      } else {
+        add({a.m > b.m ? a.m - b.m : b.m - a.m, 0});
+        add({a.m + b.m, 0});
+      }
+    }
+  }
+}
+
+o2mi::generic::Geom generic_geom(const o2mi_tp_plan* p, int64_t n_rows) {
+  o2mi::generic::Geom g{};
+  g.n_rows = n_rows;
+  g.weight_numel = p->weight_numel;
+  g.channels = p->channels;
+  g.width = (int)p->width;
+  g.lanes = p->full ? 2 * p->channels : p->channels;
+  g.full = p->full;
+  g.layout = p->layout;
+  g.n_keys = p->n_keys;
+  g.n_paths = p->n_paths;
+  return g;
+}
+
+struct TablesShape {
+  o2mi::generic::WeightShape weight;
+  int64_t splits;
+  size_t bytes;
+};
+
+TablesShape tables_shape(const o2mi_tp_plan* p, int64_t n_rows) {
+  TablesShape t{};
+  t.weight = o2mi::generic::weight_shape(generic_geom(p, n_rows), device_cus());
+  const int64_t rows = t.weight.groups;
+  t.splits = rows <= kReduceSplitRows
+                 ? 1
+                 : std::min<int64_t>(64, (rows + kReduceSplitRows - 1) / kReduceSplitRows);
+  const int64_t floats = (rows + (t.splits > 1 ? t.splits : 0)) * p->weight_numel;
+  t.bytes = n_rows > 0 ? (size_t)floats * sizeof(float) : 0;
+  return t;
+}
+
+// dw = fixed-order column sum of `rows` partial rows (one or two passes).
+hipError_t reduce_partials(float* partial, int64_t rows, int64_t splits, int64_t pw, float* dw,
+                           hipStream_t s) {
+  if (splits == 1) return column_sum(partial, rows, pw, 1, dw, s);
+  float* second = partial + rows * pw;
+  hipError_t err = column_sum(partial, rows, pw, splits, second, s);
+  if (err == hipSuccess) err = column_sum(second, splits, pw, 1, dw, s);
+  return err;
+}
+
 // Shared body of the backward entry points.  `fit_grid`: shrink the grid so
 // that the partial rows fit in `workspace_bytes` instead of failing.
 int tp_backward(const o2mi_tp_plan* plan, const float* x, const float* y, const float* w,
@@ -306,6 +396,8 @@ int tp_backward(const o2mi_tp_plan* plan, const float* x, const float* y, const 
     return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
   if (n_rows > (int64_t)INT32_MAX * 64)
     return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  if (!plan->set)
+    return fail(O2MI_ERR_UNSUPPORTED, "no compiled kernels for this plan: use o2mi_tp_backward_tables_f32");
   const int variant = pick_variant(plan, {x, y, g, (needed & 1) ? dx : nullptr,
                                           (needed & 2) ? dy : nullptr});
   const bool fit = fit_grid && (needed & 4);
@@ -322,14 +414,7 @@ int tp_backward(const o2mi_tp_plan* plan, const float* x, const float* y, const 
   if (timing) o2mi_timing_end(s, &timed);
   if (err != hipSuccess) return fail_hip(err, "tp backward launch");
   if (needed & 4) {
-    const int64_t pw = plan->weight_numel;
-    if (shape.splits == 1) {
-      err = column_sum(partial, shape.partial_rows, pw, 1, dw, s);
-    } else {
-      float* second = partial + shape.partial_rows * pw;
-      err = column_sum(partial, shape.partial_rows, pw, shape.splits, second, s);
-      if (err == hipSuccess) err = column_sum(second, shape.splits, pw, 1, dw, s);
-    }
+    err = reduce_partials(partial, shape.partial_rows, shape.splits, plan->weight_numel, dw, s);
     if (err != hipSuccess) return fail_hip(err, "dw reduction launch");
   }
   return O2MI_OK;
@@ -409,14 +494,19 @@ int o2mi_tp_plan_create(int channels, int m_max, int parity, int normalization, 
                          (layout == O2MI_LAYOUT_COMPONENT_MAJOR && !full) ||
                          (layout == O2MI_LAYOUT_COPY_COMPONENT_MAJOR && full);
   if (!layout_ok) return fail(O2MI_ERR_INVALID_ARGUMENT, "layout does not match the parity");
+  // Without compiled kernels the plan is table-driven only
+  // (o2mi_tp_forward_tables_f32 / o2mi_tp_backward_tables_f32).
   const o2mi::TPKernelSet* set = o2mi_find_tp_set(m_max, full ? 1 : 0, normalization);
-  if (!set) return fail(O2MI_ERR_UNSUPPORTED, "no kernels compiled for this m_max/parity/normalization");
+  const int n_keys = (full ? 2 : 1) + m_max;
+  if (!set && n_keys > o2mi::generic::max_keys())
+    return fail(O2MI_ERR_UNSUPPORTED, "m_max beyond the table-driven kernels' limit");
   // Row width and packed weight count in units of C.
-  int width_units = 0;
-  for (int k = 0; k < set->table.n_keys; ++k) {
-    const o2mi::KeySpec& ks = set->table.keys[k];
-    width_units = std::max(width_units, ks.off + (ks.dim == 1 ? 1 : (full ? 4 : 2)));
-  }
+  const int width_units = (full ? 2 : 1) + m_max * (full ? 4 : 2);
+  int n_paths = 0;
+  int64_t units = 0;
+  count_paths(m_max, full, &n_paths, &units);
+  if (set && (set->table.n_paths != n_paths || set->table.n_units != units))
+    return fail(O2MI_ERR_UNSUPPORTED, "compiled plan disagrees with the selection rules");
   o2mi_tp_plan* p = new (std::nothrow) o2mi_tp_plan;
   if (!p) return fail(O2MI_ERR_INVALID_ARGUMENT, "out of host memory");
   p->set = set;
@@ -426,7 +516,9 @@ int o2mi_tp_plan_create(int channels, int m_max, int parity, int normalization, 
   p->normalization = normalization;
   p->layout = layout;
   p->width = (int64_t)width_units * channels;
-  p->weight_numel = (int64_t)set->table.n_units * channels;
+  p->weight_numel = units * channels;
+  p->n_keys = n_keys;
+  p->n_paths = n_paths;
   if (p->width * 8 >= (int64_t)INT32_MAX || p->weight_numel >= (int64_t)INT32_MAX / 4096) {
     delete p;
     return fail(O2MI_ERR_INVALID_ARGUMENT, "channels too large");
@@ -439,6 +531,8 @@ int o2mi_tp_plan_destroy(o2mi_tp_plan* plan) {
   delete plan;
   return O2MI_OK;
 }
+
+int o2mi_tp_plan_compiled(const o2mi_tp_plan* plan) { return plan ? (plan->set ? 1 : 0) : -1; }
 
 int64_t o2mi_tp_width(const o2mi_tp_plan* plan) { return plan ? plan->width : -1; }
 
@@ -484,6 +578,8 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
   if (!x || !y || !w || !out) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
   if (n_rows > (int64_t)INT32_MAX * 64)
     return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  if (!plan->set)
+    return fail(O2MI_ERR_UNSUPPORTED, "no compiled kernels for this plan: use o2mi_tp_forward_tables_f32");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int variant = pick_variant(plan, {x, y, out});
   const int64_t target =
@@ -501,6 +597,7 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
 int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward, int* grid,
                          int* blocks_per_cu, int* rows_per_iter, int* tiles) {
   if (!plan || n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "bad plan or n_rows");
+  if (!plan->set) return fail(O2MI_ERR_UNSUPPORTED, "no compiled kernels for this plan");
   const int variant = plan->layout == O2MI_LAYOUT_CHANNEL_MAJOR ? o2mi::kVariantChannelMajorVec2
                                                                 : o2mi::kVariantComponentMajor;
   const int per_cu = plan->set->blocks_per_cu(variant, backward != 0);
@@ -516,7 +613,7 @@ int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward,
 }
 
 size_t o2mi_tp_backward_workspace_bytes(const o2mi_tp_plan* plan, int64_t n_rows) {
-  if (!plan || n_rows <= 0) return 0;
+  if (!plan || n_rows <= 0 || !plan->set) return 0;
   // The variant only changes the occupancy query; size for the largest.
   size_t bytes = 0;
   for (int v = 0; v < o2mi::kNumVariants; ++v) {
@@ -546,6 +643,80 @@ int o2mi_tp_backward_noalloc_f32(const o2mi_tp_plan* plan, const float* x, const
   }
   return tp_backward(plan, x, y, w, g, dx, dy, dw, partial, O2MI_TP_SCRATCH_BYTES, true, n_rows,
                      needed, stream);
+}
+
+int o2mi_tp_forward_tables_f32(const o2mi_tp_plan* plan, const float* x, const float* y,
+                               const float* w, const int32_t* path_info,
+                               const float* path_coefficients, int n_paths, float* out,
+                               int64_t n_rows, void* stream) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
+  if (n_paths != plan->n_paths)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "path table does not have the plan's path count");
+  if (n_rows == 0) return O2MI_OK;
+  if (!x || !y || !w || !out || !path_info || !path_coefficients)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (n_rows > (int64_t)INT32_MAX * 64) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_FORWARD);
+  const hipError_t err = o2mi::generic::forward(x, y, w, out, path_info, path_coefficients,
+                                                generic_geom(plan, n_rows), device_cus(), s);
+  if (timing) o2mi_timing_end(s, &timed);
+  if (err != hipSuccess) return fail_hip(err, "table-driven tp forward launch");
+  return O2MI_OK;
+}
+
+size_t o2mi_tp_backward_tables_workspace_bytes(const o2mi_tp_plan* plan, int64_t n_rows) {
+  if (!plan || n_rows <= 0) return 0;
+  return tables_shape(plan, n_rows).bytes;
+}
+
+int o2mi_tp_backward_tables_f32(const o2mi_tp_plan* plan, const float* x, const float* y,
+                                const float* w, const float* g, const int32_t* path_info,
+                                const float* path_coefficients, int n_paths, float* dx,
+                                float* dy, float* dw, void* workspace, size_t workspace_bytes,
+                                int64_t n_rows, int needed, void* stream) {
+  if (!plan) return fail(O2MI_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (n_rows < 0) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows must be non-negative");
+  if (needed & ~7) return fail(O2MI_ERR_INVALID_ARGUMENT, "needed must be a mask of 1, 2, 4");
+  if ((needed & 4) && !dw) return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL dw for a requested gradient");
+  if (n_paths != plan->n_paths)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "path table does not have the plan's path count");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_rows == 0 || needed == 0) {
+    if (needed & 4) {
+      const hipError_t err = fill(dw, plan->weight_numel, 0.f, s);
+      if (err != hipSuccess) return fail_hip(err, "dw fill");
+    }
+    return O2MI_OK;
+  }
+  if (!x || !y || !w || !g || !path_info || !path_coefficients)
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL input pointer");
+  if (((needed & 1) && !dx) || ((needed & 2) && !dy))
+    return fail(O2MI_ERR_INVALID_ARGUMENT, "NULL output for a requested gradient");
+  if (n_rows > (int64_t)INT32_MAX * 64) return fail(O2MI_ERR_INVALID_ARGUMENT, "n_rows too large");
+  const o2mi::generic::Geom geom = generic_geom(plan, n_rows);
+  const TablesShape shape = tables_shape(plan, n_rows);
+  if ((needed & 4) && (!workspace || workspace_bytes < shape.bytes))
+    return fail(O2MI_ERR_WORKSPACE, "workspace smaller than o2mi_tp_backward_tables_workspace_bytes");
+  O2miTimed timed;
+  const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_BACKWARD);
+  hipError_t err = hipSuccess;
+  if (needed & 3)
+    err = o2mi::generic::input_adjoint(x, y, w, g, dx, dy, path_info, path_coefficients, geom,
+                                       needed, device_cus(), s);
+  float* partial = static_cast<float*>(workspace);
+  if (err == hipSuccess && (needed & 4))
+    err = o2mi::generic::weight_adjoint(x, y, g, partial, path_info, path_coefficients, geom,
+                                        shape.weight, s);
+  if (timing) o2mi_timing_end(s, &timed);
+  if (err != hipSuccess) return fail_hip(err, "table-driven tp backward launch");
+  if (needed & 4) {
+    err = reduce_partials(partial, shape.weight.groups, shape.splits, plan->weight_numel, dw, s);
+    if (err != hipSuccess) return fail_hip(err, "dw reduction launch");
+  }
+  return O2MI_OK;
 }
 
 }  // extern "C"

@@ -50,6 +50,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.o2mi_tp_plan_create.argtypes = [c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(vp)]
     lib.o2mi_tp_plan_destroy.restype = c_int
     lib.o2mi_tp_plan_destroy.argtypes = [vp]
+    lib.o2mi_tp_plan_compiled.restype = c_int
+    lib.o2mi_tp_plan_compiled.argtypes = [vp]
+    lib.o2mi_tp_forward_tables_f32.restype = c_int
+    lib.o2mi_tp_forward_tables_f32.argtypes = [vp, fp, fp, fp, vp, fp, c_int, fp, c_i64, vp]
+    lib.o2mi_tp_backward_tables_workspace_bytes.restype = c_sz
+    lib.o2mi_tp_backward_tables_workspace_bytes.argtypes = [vp, c_i64]
+    lib.o2mi_tp_backward_tables_f32.restype = c_int
+    lib.o2mi_tp_backward_tables_f32.argtypes = [vp, fp, fp, fp, fp, vp, fp, c_int, fp, fp, fp, vp,
+                                                c_sz, c_i64, c_int, vp]
     lib.o2mi_tp_width.restype = c_i64
     lib.o2mi_tp_width.argtypes = [vp]
     lib.o2mi_tp_weight_numel.restype = c_i64
@@ -166,6 +175,9 @@ class TPNativePlan:
         self.handle = handle
         self.width = int(lib.o2mi_tp_width(handle))
         self.weight_numel = int(lib.o2mi_tp_weight_numel(handle))
+        # Plans beyond the compiled m_max run the table-driven kernels, which
+        # read the op's path_info / path_coefficients device tables.
+        self.compiled = lib.o2mi_tp_plan_compiled(handle) == 1
 
     def __del__(self):
         handle = getattr(self, "handle", None)
@@ -197,6 +209,31 @@ class TPNativePlan:
         check(self._lib.o2mi_tp_backward_f32(self.handle, x, y, w, g, dx, dy, dw, workspace,
                                              workspace_bytes, n_rows, needed, stream),
               "o2mi_tp_backward_f32")
+
+
+class TablesCall:
+    """Table-driven entry points of a plan (any m_max)."""
+
+    def __init__(self, plan: TPNativePlan, path_info, path_coefficients, n_paths: int):
+        self.plan, self.info, self.coef, self.n_paths = plan, path_info, path_coefficients, n_paths
+
+    def forward(self, x, y, w, out, n_rows: int, stream: int) -> None:
+        lib = self.plan._lib
+        check(lib.o2mi_tp_forward_tables_f32(self.plan.handle, x, y, w, self.info, self.coef,
+                                             self.n_paths, out, n_rows, stream),
+              "o2mi_tp_forward_tables_f32")
+
+    def workspace_bytes(self, n_rows: int) -> int:
+        return int(self.plan._lib.o2mi_tp_backward_tables_workspace_bytes(self.plan.handle,
+                                                                          n_rows))
+
+    def backward(self, x, y, w, g, dx, dy, dw, workspace, workspace_bytes: int, n_rows: int,
+                 needed: int, stream: int) -> None:
+        lib = self.plan._lib
+        check(lib.o2mi_tp_backward_tables_f32(self.plan.handle, x, y, w, g, self.info, self.coef,
+                                              self.n_paths, dx, dy, dw, workspace,
+                                              workspace_bytes, n_rows, needed, stream),
+              "o2mi_tp_backward_tables_f32")
 
 
 def compiled_table(m_max: int, parity: str, normalization: str):

@@ -80,6 +80,25 @@ def _check_inputs(*tensors: torch.Tensor) -> None:
             raise ValueError("o2 ops need contiguous tensors")
 
 
+def _launcher(native: _native.TPNativePlan, path_info: torch.Tensor,
+              path_coefficients: torch.Tensor, device: torch.device):
+    """The compiled kernels of the plan, or (m_max beyond the compiled plans)
+    the table-driven kernels reading the op's own path tables on ``device``."""
+    if native.compiled:
+        return native
+    n_paths = path_info.shape[0] if path_info.dim() == 2 else -1
+    if (path_info.dtype != torch.int32 or path_info.dim() != 2 or path_info.shape[1] != 25
+            or path_coefficients.dtype != torch.float32
+            or tuple(path_coefficients.shape) != (n_paths, 4)):
+        raise ValueError("path_info / path_coefficients must be int32 [P, 25] / float32 [P, 4]")
+    if path_info.device != device or path_coefficients.device != device:
+        raise ValueError("the path tables must be on the operands' device")
+    info, coef = path_info.contiguous(), path_coefficients.contiguous()
+    call = _native.TablesCall(native, info.data_ptr(), coef.data_ptr(), n_paths)
+    call.keep = (info, coef)
+    return call
+
+
 def _check_shapes(op: str, native, left, right, weight, grad_output=None) -> None:
     """The kernels read x, y (and the cotangent) as [N, W] rows and w as P_w
     floats: anything else is refused before a launch."""
@@ -103,9 +122,10 @@ def o2_forward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
     _check_inputs(left, right, weight)
     n_rows = left.shape[0]
     out = torch.empty_like(left)
+    kernels = _launcher(native, path_info, path_coefficients, left.device)
     with torch.cuda.device(left.device):
-        native.forward(left.data_ptr(), right.data_ptr(), weight.data_ptr(), out.data_ptr(),
-                       n_rows, _stream(left.device))
+        kernels.forward(left.data_ptr(), right.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                        n_rows, _stream(left.device))
     return out
 
 
@@ -127,13 +147,14 @@ def o2_backward(left: torch.Tensor, right: torch.Tensor, weight: torch.Tensor,
     grad_left = torch.empty_like(left)
     grad_right = torch.empty_like(right)
     grad_weight = torch.empty_like(weight)
+    kernels = _launcher(native, path_info, path_coefficients, left.device)
     # The workspace size depends on the device's CU count: query it on the
     # tensors' device, like the launch.
     with torch.cuda.device(left.device):
-        ws_bytes = native.workspace_bytes(n_rows)
+        ws_bytes = kernels.workspace_bytes(n_rows)
         workspace = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32,
                                 device=left.device)
-        native.backward(left.data_ptr(), right.data_ptr(), weight.data_ptr(),
+        kernels.backward(left.data_ptr(), right.data_ptr(), weight.data_ptr(),
                         grad_output.data_ptr(), grad_left.data_ptr(), grad_right.data_ptr(),
                         grad_weight.data_ptr(), workspace.data_ptr(), ws_bytes, n_rows, 7,
                         _stream(left.device))

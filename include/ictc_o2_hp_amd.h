@@ -51,10 +51,18 @@ const char *o2mi_version(void);
  * normalization) with flat layout `layout`.  Replaces the per-module
  * metadata registration of triton_o2.py:1098-1132 (_METADATA / metadata_id)
  * and the layout override of triton_o2.py:1226-1234.  A plan may be shared
- * by threads. */
+ * by threads.  Plans with m_max <= 6 have compiled kernels
+ * (o2mi_tp_forward_f32 / o2mi_tp_backward_f32); larger m_max (up to 46 full,
+ * 47 canonical) give table-driven plans, which only the *_tables_* entry
+ * points run (the compiled ones return O2MI_ERR_UNSUPPORTED for them). */
 int o2mi_tp_plan_create(int channels, int m_max, int parity, int normalization,
                         int layout, o2mi_tp_plan **plan);
 int o2mi_tp_plan_destroy(o2mi_tp_plan *plan);
+
+/* 1 if the plan has compiled kernels (o2mi_tp_forward_f32 and
+ * o2mi_tp_backward_f32 run it), 0 if it is table-driven only, -1 for NULL.
+ * No counterpart in the reference (its kernels are JIT-specialised). */
+int o2mi_tp_plan_compiled(const o2mi_tp_plan *plan);
 
 /* Row width W and packed weight count P_w of the plan
  * (representation_dimension and weight.numel(), native_o2.py:137-143). */
@@ -95,6 +103,33 @@ int o2mi_tp_backward_f32(const o2mi_tp_plan *plan, const float *x, const float *
                          const float *w, const float *g, float *dx, float *dy,
                          float *dw, void *workspace, size_t workspace_bytes,
                          int64_t n_rows, int needed, void *stream);
+
+/* Table-driven forward for any plan, including plans without compiled
+ * kernels (m_max >= 7; o2mi_tp_plan_create accepts m_max up to 46 in full
+ * parity, 47 in canonical).  Replaces the o2_forward op (triton_o2.py:786-875)
+ * for plans the reference JIT-specialises (triton_o2.py:1098-1132): the path
+ * table is the op's own device metadata, path_info int32 [n_paths, 25] and
+ * path_coefficients f32 [n_paths, 4] as built by runtime_weight.py:14-29
+ * (weight_metadata), with n_paths the plan's path count.  Same layouts and
+ * results as o2mi_tp_forward_f32. */
+int o2mi_tp_forward_tables_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
+                               const float *w, const int32_t *path_info,
+                               const float *path_coefficients, int n_paths, float *out,
+                               int64_t n_rows, void *stream);
+
+/* Bytes of workspace o2mi_tp_backward_tables_f32 needs for n_rows rows. */
+size_t o2mi_tp_backward_tables_workspace_bytes(const o2mi_tp_plan *plan, int64_t n_rows);
+
+/* Table-driven VJP for any plan: the o2_backward op (triton_o2.py:878-966)
+ * with the runtime-table weight adjoint of runtime_weight.py:54-91.  dx, dy
+ * and the dw partial rows are separate passes; dw is a fixed-order sum
+ * (bitwise reproducible).  Arguments as o2mi_tp_backward_f32 plus the path
+ * table of o2mi_tp_forward_tables_f32. */
+int o2mi_tp_backward_tables_f32(const o2mi_tp_plan *plan, const float *x, const float *y,
+                                const float *w, const float *g, const int32_t *path_info,
+                                const float *path_coefficients, int n_paths, float *dx,
+                                float *dy, float *dw, void *workspace, size_t workspace_bytes,
+                                int64_t n_rows, int needed, void *stream);
 
 /* Bytes of the library-owned device scratch of o2mi_tp_backward_noalloc_f32
  * (one array per GPU, held until the process ends). */

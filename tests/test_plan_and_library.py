@@ -113,8 +113,8 @@ def test_plan_create_validates_arguments(lib):
     assert lib.o2mi_tp_plan_create(8, -1, 0, 0, 0, ctypes.byref(handle)) == -1
     assert lib.o2mi_tp_plan_create(8, 2, 3, 0, 0, ctypes.byref(handle)) == -1
     assert lib.o2mi_tp_plan_create(8, 2, 1, 0, 1, ctypes.byref(handle)) == -1   # layout/parity
-    assert lib.o2mi_tp_plan_create(8, 99, 1, 0, 0, ctypes.byref(handle)) == -2  # not compiled
-    assert b"compiled" in lib.o2mi_last_error()
+    assert lib.o2mi_tp_plan_create(8, 99, 1, 0, 0, ctypes.byref(handle)) == -2  # beyond the limit
+    assert b"table-driven" in lib.o2mi_last_error()
     plan = _native.TPNativePlan(128, 6, "full", "component", 0)
     assert (plan.width, plan.weight_numel) == (3328, 19712)
     plan = _native.TPNativePlan(5, 4, "canonical", "norm", 1)
@@ -143,3 +143,19 @@ def test_tp_ops_refuse_mismatched_shapes_before_launch(lib):
         ops.o2_forward(x, x[:2], w, *meta)
     with pytest.raises(ValueError, match="shapes do not match"):
         ops.o2_forward(x, x, w[:-1], *meta)
+
+
+def test_plans_beyond_compiled_orders_are_table_driven(lib):
+    """m_max >= 7 plans are created table-driven (width and P_w from the
+    selection rules, equal to the host plan); the key limit is 48."""
+    from ictc_o2_hp import _native
+    from ictc_o2_hp.plan import TPPlan
+    for c, m, parity in ((16, 7, "full"), (5, 8, "canonical"), (3, 10, "full"),
+                         (2, 46, "full"), (2, 47, "canonical"), (32, 6, "full")):
+        native = _native.TPNativePlan(c, m, parity, "component", 0)
+        host = TPPlan(c, m, parity)
+        assert (native.width, native.weight_numel) == (host.width, host.weight_numel)
+        assert native.compiled == (m <= 6)
+    for m, parity in ((47, 1), (48, 0)):
+        handle = ctypes.c_void_p()
+        assert lib.o2mi_tp_plan_create(2, m, parity, 0, 0, ctypes.byref(handle)) == -2

@@ -357,3 +357,102 @@ def test_component_major_matches_reference_layout_vectors():
         got = _run(module, data[f"{name}/x"], data[f"{name}/y"], data[f"{name}/g"])
         for key, value in zip(("out", "dx", "dy", "dw"), got):
             assert O.normalized_error(data[f"{name}/{key}"], value) <= TOL, (name, key)
+
+
+# m_max beyond the compiled plans: the table-driven kernels, which read the
+# module's path_info / path_coefficients tables (the reference JIT-specialises
+# any m_max, triton_o2.py:1098-1132).
+TABLE_DRIVEN = [
+    # C, M, parity, normalization, N, layout class
+    (16, 7, "full", "component", 300, None),
+    (16, 8, "canonical", "component", 257, None),
+    (5, 7, "canonical", "norm", 40, None),           # odd C
+    (9, 10, "full", "norm", 33, None),
+    (24, 7, "full", "component", 64, "component_major"),
+    (7, 9, "canonical", "component", 50, "component_major"),
+]
+
+
+@pytest.mark.parametrize("channels,m_max,parity,normalization,n_rows,layout", TABLE_DRIVEN)
+def test_table_driven_plans_match_oracle(channels, m_max, parity, normalization, n_rows, layout):
+    from ictc_o2_hp import ComponentMajorTensorProduct
+    rng = np.random.default_rng(700 + channels + m_max)
+    plan = O.OraclePlan(channels, m_max, parity, normalization)
+    cls = ComponentMajorTensorProduct if layout else None
+    module = _module(channels, m_max, parity, normalization, layout_cls=cls)
+    assert module._on_kernels(torch.zeros(1, device="cuda"))
+    x, y, g = (rng.standard_normal((n_rows, plan.width)) for _ in range(3))
+    lay = 0 if not layout else (1 if parity == "canonical" else 2)
+    _check(plan, module, x, y, g, layout=lay)
+
+
+def test_table_driven_rows_at_scale():
+    """m7 full C32 at N = 65536 (many row groups of the weight adjoint): 256
+    random rows against the oracle, dw from a cotangent masked to them."""
+    rng = np.random.default_rng(7007)
+    plan = O.OraclePlan(32, 7, "full")
+    module = _module(32, 7, "full")
+    n = 65536
+    x, y, g = (rng.standard_normal((n, plan.width)) for _ in range(3))
+    rows = np.sort(rng.choice(n, 256, replace=False))
+    _check(plan, module, x, y, g, rows=rows)
+
+
+@pytest.mark.parametrize("channels,m_max,parity,normalization,layout", [
+    (32, 6, "full", "component", 0),
+    (17, 3, "full", "norm", 0),
+    (5, 4, "canonical", "component", 1),
+    (24, 5, "full", "component", 2),
+    (64, 2, "canonical", "norm", 0),
+    (130, 1, "full", "component", 0),
+])
+def test_table_driven_kernels_match_compiled_kernels(channels, m_max, parity, normalization,
+                                                     layout):
+    """For compiled plans, the table-driven entry points give the compiled
+    kernels' results (within fp32 rounding: the two sum the terms in
+    different orders), through the C ABI with the module's own tables."""
+    from ictc_o2_hp import _native
+    from ictc_o2_hp.native_o2 import _path_metadata
+    from ictc_o2_hp.plan import TPPlan
+    print(f"case tables vs compiled C{channels} m{m_max} {parity} {normalization} "
+          f"layout {layout}", flush=True)
+    native = _native.TPNativePlan(channels, m_max, parity, normalization, layout)
+    assert native.compiled
+    info, coef = (t.cuda() for t in _path_metadata(TPPlan(channels, m_max, parity,
+                                                          normalization), layout))
+    tables = _native.TablesCall(native, info.data_ptr(), coef.data_ptr(), info.shape[0])
+    gen = torch.Generator(device="cuda").manual_seed(channels + m_max)
+    n = 3001
+    x, y, g = (torch.randn((n, native.width), device="cuda", generator=gen) for _ in range(3))
+    w = torch.randn(native.weight_numel, device="cuda", generator=gen)
+    stream = torch.cuda.current_stream().cuda_stream
+    results = []
+    for kernels in (native, tables):
+        out, dx, dy = (torch.empty_like(x) for _ in range(3))
+        dw = torch.empty_like(w)
+        kernels.forward(x.data_ptr(), y.data_ptr(), w.data_ptr(), out.data_ptr(), n, stream)
+        ws_bytes = kernels.workspace_bytes(n)
+        ws = torch.empty(max(1, ws_bytes // 4), device="cuda")
+        kernels.backward(x.data_ptr(), y.data_ptr(), w.data_ptr(), g.data_ptr(), dx.data_ptr(),
+                         dy.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws_bytes, n, 7, stream)
+        results.append([t.double().cpu().numpy() for t in (out, dx, dy, dw)])
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "dx", "dy", "dw"), *results):
+        assert O.normalized_error(a, b) <= 1e-6, name
+
+
+def test_table_driven_backward_roles_and_reproducible():
+    """Role subsets of the table-driven backward and bitwise repeatable dw."""
+    torch.manual_seed(3)
+    module = _module(8, 7, "full")
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn((500, module.representation_dimension), device="cuda", generator=gen)
+    y = torch.randn(x.shape, device="cuda", generator=gen)
+    g = torch.randn(x.shape, device="cuda", generator=gen)
+    xr, yr = x.clone().requires_grad_(), y.clone().requires_grad_()
+    full = torch.autograd.grad(module(xr, yr), (xr, yr, module.weight), g)
+    again = torch.autograd.grad(module(xr, yr), (xr, yr, module.weight), g)
+    for a, b in zip(full, again):
+        assert torch.equal(a, b)
+    (dy_only,) = torch.autograd.grad(module(x, yr), (yr,), g)
+    assert torch.equal(dy_only, full[1])
