@@ -94,32 +94,51 @@ int fail_hip(hipError_t err, const char* where) {
   return O2MI_ERR_HIP;
 }
 
-constexpr int kReduceCols = 64;      // columns per reduction block (one per lane)
-constexpr int kReduceSplitRows = 64;  // rows per reduction block in the first pass
+constexpr int kReduceCols = 64;        // columns per reduction block (one per lane)
+constexpr int kReduceWaves = 16;       // waves per reduction block
+constexpr int kReduceOnePass = 2048;   // at most this many rows: one pass
+constexpr int kReduceSplitRows = 1024; // rows per first-pass split above that
 
 // out[s * ncols + col] = sum of in[r * ncols + col] over the rows of split s.
-// Each of the 4 waves sums an interleaved quarter of the rows in order, then
-// the quarters are combined as (q0 + q1) + (q2 + q3): a fixed order.
-__global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ in,
-                                                         int64_t nrows, int64_t ncols,
-                                                         int64_t rows_per_split,
-                                                         float* __restrict__ out) {
-  __shared__ float quarter[4][kReduceCols];
+// Wave w adds rows r0 + w, r0 + w + 16, ... in increasing order (four loads in
+// flight); the 16 wave sums are then combined in a fixed pairwise tree.  The
+// order depends only on the row count: the sum is bitwise reproducible.
+__global__ __launch_bounds__(kReduceWaves * 64) void column_sum_kernel(
+    const float* __restrict__ in, int64_t nrows, int64_t ncols, int64_t rows_per_split,
+    float* __restrict__ out) {
+  __shared__ float part[kReduceWaves][kReduceCols];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t col = (int64_t)blockIdx.x * kReduceCols + lane;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per_split;
   const int64_t r1 = min(nrows, r0 + rows_per_split);
+  constexpr int W = kReduceWaves;
   float s = 0.f;
   if (col < ncols) {
-    for (int64_t r = r0 + wave; r < r1; r += 4) s += in[r * ncols + col];
+    const float* p = in + col;
+    int64_t r = r0 + wave;
+    for (; r + 3 * W < r1; r += 4 * W) {
+      const float a = p[r * ncols], b = p[(r + W) * ncols];
+      const float c = p[(r + 2 * W) * ncols], d = p[(r + 3 * W) * ncols];
+      s += a;
+      s += b;
+      s += c;
+      s += d;
+    }
+    for (; r < r1; r += W) s += p[r * ncols];
   }
-  quarter[wave][lane] = s;
+  part[wave][lane] = s;
   __syncthreads();
-  if (wave == 0 && col < ncols) {
-    out[(int64_t)blockIdx.y * ncols + col] =
-        (quarter[0][lane] + quarter[1][lane]) + (quarter[2][lane] + quarter[3][lane]);
+  for (int half = W / 2; half >= 1; half /= 2) {
+    if (wave < half) part[wave][lane] += part[wave + half][lane];
+    __syncthreads();
   }
+  if (wave == 0 && col < ncols) out[(int64_t)blockIdx.y * ncols + col] = part[0][lane];
+}
+
+// First-pass splits of a fixed-order column sum over `rows` rows (1: one pass).
+int64_t reduce_splits(int64_t rows) {
+  return rows <= kReduceOnePass ? 1 : (rows + kReduceSplitRows - 1) / kReduceSplitRows;
 }
 
 __global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ out, int64_t n, float v) {
@@ -183,11 +202,12 @@ int pick_variant(const o2mi_tp_plan* p, std::initializer_list<const void*> ptrs)
   return aligned ? o2mi::kVariantChannelMajorVec2 : o2mi::kVariantChannelMajor;
 }
 
-// Rows and lanes per block, rows per block, and the grid for `n_rows` rows
-// when at most `target_blocks` blocks should be resident and a block covers at
-// most `tile` lanes of a row.
-o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_blocks, int tile,
-                      int* grid) {
+// Lanes per block, rows per block iteration and the grid for `n_rows` rows
+// when at most `target_blocks` blocks should be resident, a block has
+// `threads` threads and covers at most `tile` lanes of a row.  Blocks take
+// row chunks round-robin (strided order, o2mi_tp.hpp row_schedule).
+o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_blocks, int threads,
+                      int tile, int* grid) {
   o2mi::TPGeom g{};
   g.n_rows = n_rows;
   g.channels = p->channels;
@@ -196,26 +216,18 @@ o2mi::TPGeom geometry(const o2mi_tp_plan* p, int64_t n_rows, int64_t target_bloc
   g.lanes = p->full ? 2 * p->channels : p->channels;
   if (g.lanes <= tile) {
     g.tile_lanes = g.lanes;
-    g.rows_per_iter = o2mi::kBlock / g.lanes;
+    g.rows_per_iter = threads / g.lanes;
     g.tiles = 1;
   } else {
     g.tile_lanes = tile;
-    g.rows_per_iter = o2mi::kBlock / tile;
+    g.rows_per_iter = threads / tile;
     g.tiles = (g.lanes + tile - 1) / tile;
   }
   const int64_t r = g.rows_per_iter;
   const int64_t iterations = std::max<int64_t>(1, (n_rows + r - 1) / r);
   const int64_t max_groups = std::max<int64_t>(1, target_blocks / g.tiles);
-  const int64_t groups = std::min(max_groups, iterations);
-  const int64_t iters_per_group = (iterations + groups - 1) / groups;
-  g.rows_per_group = iters_per_group * r;
-  // Contiguous order: every group gets iters_per_group iterations; strided
-  // order: groups take iterations round-robin.
-  const int64_t used_groups = O2MI_ROW_ORDER == 1
-                                  ? groups
-                                  : (iterations + iters_per_group - 1) / iters_per_group;
-  g.groups = used_groups;
-  *grid = (int)(used_groups * g.tiles);
+  g.groups = std::min(max_groups, iterations);
+  *grid = (int)(g.groups * g.tiles);
   return g;
 }
 
@@ -232,11 +244,9 @@ BackwardShape backward_shape_for(const o2mi_tp_plan* p, int64_t n_rows, int vari
                                  int64_t target) {
   BackwardShape s{};
   s.variant = variant;
-  s.geom = geometry(p, n_rows, target, o2mi::kBackwardTile, &s.grid);
+  s.geom = geometry(p, n_rows, target, o2mi::kBackwardBlock, o2mi::kBackwardTile, &s.grid);
   s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
-  s.splits = s.partial_rows <= kReduceSplitRows
-                 ? 1
-                 : std::min<int64_t>(64, (s.partial_rows + kReduceSplitRows - 1) / kReduceSplitRows);
+  s.splits = reduce_splits(s.partial_rows);
   const int64_t floats = (s.partial_rows + (s.splits > 1 ? s.splits : 0)) * p->weight_numel;
   s.bytes = n_rows > 0 ? (size_t)floats * sizeof(float) : 0;
   return s;
@@ -247,8 +257,7 @@ BackwardShape backward_shape_for(const o2mi_tp_plan* p, int64_t n_rows, int vari
 // not fit even with one row group comes back with bytes > max_bytes.
 BackwardShape backward_shape(const o2mi_tp_plan* p, int64_t n_rows, int variant,
                              size_t max_bytes = SIZE_MAX) {
-  const int64_t target =
-      (int64_t)p->set->blocks_per_cu(variant, true) * device_cus() * O2MI_BWD_BLOCKS_MULT;
+  const int64_t target = (int64_t)p->set->blocks_per_cu(variant, true) * device_cus();
   BackwardShape s = backward_shape_for(p, n_rows, variant, target);
   if (s.bytes <= max_bytes) return s;
   // Bytes grow with the number of row groups: bisect on it.
@@ -280,7 +289,8 @@ hipError_t column_sum(const float* in, int64_t nrows, int64_t ncols, int64_t spl
                       hipStream_t stream) {
   const int64_t per_split = (nrows + splits - 1) / splits;
   dim3 grid((unsigned)((ncols + kReduceCols - 1) / kReduceCols), (unsigned)splits);
-  hipLaunchKernelGGL(column_sum_kernel, grid, dim3(256), 0, stream, in, nrows, ncols, per_split,
+  hipLaunchKernelGGL(column_sum_kernel, grid, dim3(kReduceWaves * 64), 0, stream, in, nrows, ncols,
+                     per_split,
                      out);
   return hipGetLastError();
 }
@@ -354,9 +364,7 @@ TablesShape tables_shape(const o2mi_tp_plan* p, int64_t n_rows) {
   TablesShape t{};
   t.weight = o2mi::generic::weight_shape(generic_geom(p, n_rows), device_cus());
   const int64_t rows = t.weight.groups;
-  t.splits = rows <= kReduceSplitRows
-                 ? 1
-                 : std::min<int64_t>(64, (rows + kReduceSplitRows - 1) / kReduceSplitRows);
+  t.splits = reduce_splits(rows);
   const int64_t floats = (rows + (t.splits > 1 ? t.splits : 0)) * p->weight_numel;
   t.bytes = n_rows > 0 ? (size_t)floats * sizeof(float) : 0;
   return t;
@@ -582,10 +590,10 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
     return fail(O2MI_ERR_UNSUPPORTED, "no compiled kernels for this plan: use o2mi_tp_forward_tables_f32");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int variant = pick_variant(plan, {x, y, out});
-  const int64_t target =
-      (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus() * O2MI_FWD_BLOCKS_MULT;
+  const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
   int grid = 0;
-  const o2mi::TPGeom g = geometry(plan, n_rows, target, o2mi::kForwardTile, &grid);
+  const o2mi::TPGeom g =
+      geometry(plan, n_rows, target, o2mi::kBlock, o2mi::kForwardTile, &grid);
   O2miTimed timed;
   const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_FORWARD);
   const hipError_t err = plan->set->forward(variant, x, y, w, out, g, grid, s);
@@ -604,6 +612,7 @@ int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward,
   int g = 0;
   const o2mi::TPGeom geom =
       geometry(plan, n_rows, (int64_t)per_cu * device_cus(),
+               backward ? o2mi::kBackwardBlock : o2mi::kBlock,
                backward ? o2mi::kBackwardTile : o2mi::kForwardTile, &g);
   if (grid) *grid = g;
   if (blocks_per_cu) *blocks_per_cu = per_cu;

@@ -59,89 +59,30 @@ struct TermSpec {
   int sign;     // +1 or -1
 };
 
-// Build-time tuning knobs (defaults are the measured best).
-// Cache-policy bits of row loads and stores (1 sc0, 2 nt, 16 sc1).  Every
+// Cache policies of row loads and stores (bits: 1 sc0, 2 nt, 16 sc1).  Every
 // row is touched once per kernel, so loads are non-temporal; the forward's
 // stores are non-temporal + sc1, the backward's non-temporal (measured best
 // at the headline shape: forward 0.938 -> 0.890 ms, backward 1.722 -> 1.659
-// ms together with the reverse row order below).
-#ifndef O2MI_LOAD_CPOL
-#define O2MI_LOAD_CPOL 2
-#endif
-#ifndef O2MI_FWD_STORE_CPOL
-#define O2MI_FWD_STORE_CPOL 18
-#endif
-#ifndef O2MI_BWD_STORE_CPOL
-#define O2MI_BWD_STORE_CPOL 2
-#endif
-#ifndef O2MI_FWD_PREFETCH
-#define O2MI_FWD_PREFETCH 0  // forward loads the next iteration's rows early
-#endif
-#ifndef O2MI_FWD_WAVES
-#define O2MI_FWD_WAVES 1  // minimum waves per SIMD requested for the forward
-#endif
-#ifndef O2MI_BWD_WAVES
-#define O2MI_BWD_WAVES 2  // minimum waves per SIMD requested for the backward
-#endif
-#ifndef O2MI_FWD_TILE
-#define O2MI_FWD_TILE 256  // lanes of one row handled by a forward block
-#endif
-#ifndef O2MI_BWD_TILE
-#define O2MI_BWD_TILE 256  // lanes of one row handled by a backward block
-#endif
-// Blocks launched per resident block slot (1: persistent kernels).
-// 1: the forward keeps each lane's path weights in registers for the whole
-// (persistent) kernel instead of re-reading them from LDS every row.
-#ifndef O2MI_FWD_WREG
-#define O2MI_FWD_WREG 1
-#endif
-// Start delay, in units of s_sleep(127) (~8k cycles), of the blocks in the
-// second half of the grid (the second resident block of each CU), so that the
-// two blocks sharing a CU alternate between memory and compute phases.
-#ifndef O2MI_FWD_STAGGER
-#define O2MI_FWD_STAGGER 0
-#endif
-#ifndef O2MI_BWD_STAGGER
-#define O2MI_BWD_STAGGER 0
-#endif
-// Backward variants: weights in registers (no LDS) and/or no next-row prefetch.
-#ifndef O2MI_BWD_WREG
-#define O2MI_BWD_WREG 0
-#endif
-#ifndef O2MI_BWD_PREFETCH
-#define O2MI_BWD_PREFETCH 0
-#endif
-#ifndef O2MI_FWD_BLOCKS_MULT
-#define O2MI_FWD_BLOCKS_MULT 1
-#endif
-#ifndef O2MI_BWD_BLOCKS_MULT
-#define O2MI_BWD_BLOCKS_MULT 1
-#endif
-#ifndef O2MI_FWD_REVERSE
-#define O2MI_FWD_REVERSE 0  // 1: the forward visits row chunks from the last one down
-#endif
-// 1: the backward visits row chunks from the last one down, so it starts on
-// the rows the forward touched last (still in the memory-side cache).
-#ifndef O2MI_BWD_REVERSE
-#define O2MI_BWD_REVERSE 1
-#endif
-// Cap on resident blocks per CU used to size the persistent grids (0: the
-// occupancy limit).
-#ifndef O2MI_FWD_MAX_BLOCKS_PER_CU
-#define O2MI_FWD_MAX_BLOCKS_PER_CU 0
-#endif
-#ifndef O2MI_BWD_MAX_BLOCKS_PER_CU
-#define O2MI_BWD_MAX_BLOCKS_PER_CU 0
-#endif
-#ifndef O2MI_ROW_ORDER
-#define O2MI_ROW_ORDER 1  // 1: block b takes iterations b, b+G, ...; 0: one contiguous range
-#endif
+// ms together with the reverse row order of the backward).
+constexpr int kLoadPolicy = 2;
+constexpr int kForwardStorePolicy = 18;
+constexpr int kBackwardStorePolicy = 2;
 
+// Threads per block and the lanes of one row a block covers (a row of more
+// lanes is split over several blocks, "tiles").  The forward keeps each
+// lane's path weights in registers for the whole persistent kernel and runs
+// at up to 3 waves per SIMD; the backward holds one weight-adjoint
+// accumulator per path and lane in registers and needs 2 waves per SIMD to
+// hide its dependent FMA chains and LDS weight reads.
 constexpr int kBlock = 256;
-constexpr int kForwardTile = O2MI_FWD_TILE;
-constexpr int kBackwardTile = O2MI_BWD_TILE;
+constexpr int kBackwardBlock = 256;  // 512 (two rows per iteration, one block per CU): same time
+constexpr int kForwardTile = 256;
+constexpr int kBackwardTile = 256;
+constexpr int kForwardWaves = 1;   // minimum waves per SIMD requested
+constexpr int kBackwardWaves = 2;
 static_assert(kForwardTile % 2 == 0 && kForwardTile <= kBlock, "tile must be even, <= block");
-static_assert(kBackwardTile % 2 == 0 && kBackwardTile <= kBlock, "tile must be even, <= block");
+static_assert(kBackwardTile % 2 == 0 && kBackwardTile <= kBackwardBlock,
+              "tile must be even, <= block");
 // Byte offset given to lanes with nothing to load or store: beyond any
 // descriptor size used here (< 2^31), with room to add key offsets.
 constexpr uint32_t kIdle = 0x80000000u;
@@ -158,7 +99,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Launch geometry, computed on the host (o2mi_capi.hip).
 struct TPGeom {
   int64_t n_rows;
-  int64_t rows_per_group;  // contiguous order: rows owned by one block (multiple of rows_per_iter)
   int64_t groups;          // blocks along the rows (grid = groups * tiles)
   int channels;            // C
   int width;               // W, floats per row
@@ -221,7 +161,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, i
 
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
   return __builtin_bit_cast(float,
-                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, O2MI_LOAD_CPOL));
+                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, kLoadPolicy));
 }
 
 using f32x2 = float __attribute__((ext_vector_type(2)));
@@ -232,7 +172,7 @@ using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff,
                                        float& a, float& b) {
   const f32x2 v = __builtin_bit_cast(
-      f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, O2MI_LOAD_CPOL));
+      f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, kLoadPolicy));
   a = v.x;
   b = v.y;
 }
@@ -444,35 +384,24 @@ struct RowSchedule {
   }
 };
 
-template <int kSleeps>
-__device__ __forceinline__ void stagger_start() {
-  if constexpr (kSleeps > 0) {
-    if (blockIdx.x >= gridDim.x / 2)
-      for (int i = 0; i < kSleeps; ++i) __builtin_amdgcn_s_sleep(127);
-  }
-}
-
-template <bool kReverse = false>
+// Strided order: block b takes row chunks b, b + G, b + 2G, ... (all blocks
+// sweep one contiguous window of the tensors at any time); with kReverse the
+// chunks are taken from the last one down.
+template <bool kReverse>
 __host__ __device__ __forceinline__ RowSchedule row_schedule(const TPGeom& g, int64_t group) {
   RowSchedule s;
   s.rows_per_iter = g.rows_per_iter;
+  s.limit = g.n_rows;
   if constexpr (kReverse) {
-    // Strided order from the last row chunk down: chunk k = T-1-(b + it*G).
+    // Chunk k = T - 1 - (b + it * G).
     const int64_t chunks = (g.n_rows + g.rows_per_iter - 1) / g.rows_per_iter;
     s.first = (chunks - 1 - group) * g.rows_per_iter;
     s.step = -g.groups * g.rows_per_iter;
-    s.limit = g.n_rows;
     s.iters = group < chunks ? (int)((chunks - group + g.groups - 1) / g.groups) : 0;
-  } else if constexpr (O2MI_ROW_ORDER == 1) {
+  } else {
     s.first = group * g.rows_per_iter;
     s.step = g.groups * g.rows_per_iter;
-    s.limit = g.n_rows;
     s.iters = s.first < g.n_rows ? (int)((g.n_rows - s.first + s.step - 1) / s.step) : 0;
-  } else {
-    s.first = group * g.rows_per_group;
-    s.step = g.rows_per_iter;
-    s.limit = g.n_rows < s.first + g.rows_per_group ? g.n_rows : s.first + g.rows_per_group;
-    s.iters = s.limit > s.first ? (int)((s.limit - s.first + s.step - 1) / s.step) : 0;
   }
   return s;
 }
@@ -480,17 +409,15 @@ __host__ __device__ __forceinline__ RowSchedule row_schedule(const TPGeom& g, in
 // ---------------------------------------------------------------------------
 // Forward: out = sum over paths of w * CG(x, y)  (native_o2.py:209-221).
 template <class P, int kLayout, bool kVec2>
-__global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
+__global__ __launch_bounds__(kBlock, kForwardWaves) void tp_forward_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     float* __restrict__ out, TPGeom g) {
   constexpr int kTile = kForwardTile;
-  extern __shared__ float lds_w[];
   const int tile = blockIdx.x % g.tiles;
   const int64_t group = blockIdx.x / g.tiles;
   const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
-#if O2MI_FWD_WREG
   // This lane's weight of every path (times the coupling magnitude).
   float wreg[P::kPaths];
   static_for<P::kPaths>([&](auto pc) {
@@ -499,39 +426,14 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
     const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
     wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
   });
-#else
-  stage_weights<P, kTile>(lds_w, w, C, tile);
-  __syncthreads();
-  WeightColumns<P> col = weight_columns<P>(l);
-#endif
 
-  const RowSchedule sched = row_schedule<O2MI_FWD_REVERSE != 0>(g, group);
-  stagger_start<O2MI_FWD_STAGGER>();
+  const RowSchedule sched = row_schedule<false>(g, group);
   float X[P::kKeys][2], Y[P::kKeys][2];
-  if constexpr (O2MI_FWD_PREFETCH) {
-    load_row<P, kLayout, kVec2>(rows_rsrc(x, sched.row0(0), g.width, sched.rows(0)), C, l, o,
-                                false, X);
-    load_row<P, kLayout, kVec2>(rows_rsrc(y, sched.row0(0), g.width, sched.rows(0)), C, l, o,
-                                false, Y);
-  }
   for (int it = 0; it < sched.iters; ++it) {
     const int64_t row0 = sched.row0(it);
     const int rows = sched.rows(it);
-    float Xn[P::kKeys][2], Yn[P::kKeys][2];
-    if constexpr (O2MI_FWD_PREFETCH) {
-      const int64_t row_next = sched.row0(it + 1);
-      const int rows_next = sched.rows(it + 1);
-      load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
-      load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
-    } else {
-      load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
-      load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
-    }
-#if !O2MI_FWD_WREG
-    // Re-read the weights every iteration: keeping all of them in registers
-    // would cost occupancy.
-    asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
-#endif
+    load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
+    load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
     float A[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       A[decltype(kc)::value][0] = 0.f;
@@ -540,27 +442,14 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
-#if O2MI_FWD_WREG
       const float wv = wreg[p];
-#else
-      const float wv = staged_weight<P, kTile, p>(lds_w, col);
-#endif
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       A[ps.k3][0] = fmaf(wv, f0, A[ps.k3][0]);
       if constexpr (out_is_freq<P>(p)) A[ps.k3][1] = fmaf(wv, f1, A[ps.k3][1]);
     });
-    store_row<P, kLayout, kVec2, O2MI_FWD_STORE_CPOL>(rows_rsrc(out, row0, g.width, rows), C, l,
+    store_row<P, kLayout, kVec2, kForwardStorePolicy>(rows_rsrc(out, row0, g.width, rows), C, l,
                                                       o, A);
-    if constexpr (O2MI_FWD_PREFETCH) {
-      static_for<P::kKeys>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        X[k][0] = Xn[k][0];
-        X[k][1] = Xn[k][1];
-        Y[k][0] = Yn[k][0];
-        Y[k][1] = Yn[k][1];
-      });
-    }
   }
 }
 
@@ -570,7 +459,7 @@ __global__ __launch_bounds__(kBlock, O2MI_FWD_WAVES) void tp_forward_kernel(
 //   dy[k2][j] += w * coef * g[k3][k] * x[k1][i]
 //   dw[p, o]  += coef * x[k1][i] * y[k2][j] * g[k3][k] (triton_o2.py:571-607)
 template <class P, int kLayout, bool kVec2>
-__global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
+__global__ __launch_bounds__(kBackwardBlock, kBackwardWaves) void tp_backward_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ gout, float* __restrict__ dx, float* __restrict__ dy,
     float* __restrict__ partial, TPGeom g, int needed) {
@@ -581,77 +470,56 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
   const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
-#if O2MI_BWD_WREG
-  float wreg[P::kPaths];
-  static_for<P::kPaths>([&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    constexpr PathSpec ps = P::paths[p];
-    const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
-    wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
-  });
-#else
   stage_weights<P, kTile>(lds_w, w, C, tile);
   __syncthreads();
   WeightColumns<P> col = weight_columns<P>(l);
-#endif
 
   float dwacc[P::kPaths];
   static_for<P::kPaths>([&](auto pc) { dwacc[decltype(pc)::value] = 0.f; });
 
-  const RowSchedule sched = row_schedule<O2MI_BWD_REVERSE != 0>(g, group);
+  // Reverse order: the first rows visited are the ones the forward touched
+  // last, still in the memory-side cache.
+  const RowSchedule sched = row_schedule<true>(g, group);
   // Stores of roles that were not requested go to idle offsets (dropped).
   LaneOffsets ox = o, oy = o;
   if (!(needed & 1)) ox.scalar_own = ox.freq = kIdle;
   if (!(needed & 2)) oy.scalar_own = oy.freq = kIdle;
 
-  stagger_start<O2MI_BWD_STAGGER>();
+  // Scalar outputs belong to the copy-0 lane; the copy-1 lane reads a zero
+  // cotangent there, which removes its (wrong-copy) contributions.  The first
+  // iteration's loads are issued before the loop (measured: loading at the
+  // top of every iteration instead made the compiler schedule the loop body
+  // differently and doubled the kernel's time at the headline shape).
   float X[P::kKeys][2], Y[P::kKeys][2], G[P::kKeys][2];
   {
     const int64_t row0 = sched.row0(0);
     const int rows = sched.rows(0);
     load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
     load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
-    // Scalar outputs belong to the copy-0 lane; the copy-1 lane reads a zero
-    // cotangent there, which removes its (wrong-copy) contributions.
     load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
   }
   for (int it = 0; it < sched.iters; ++it) {
     const int64_t row0 = sched.row0(it);
     const int rows = sched.rows(it);
-#if O2MI_BWD_PREFETCH
-    const int64_t row_next = sched.row0(it + 1);
-    const int rows_next = sched.rows(it + 1);
-    float Xn[P::kKeys][2], Yn[P::kKeys][2], Gn[P::kKeys][2];
-    load_row<P, kLayout, kVec2>(rows_rsrc(x, row_next, g.width, rows_next), C, l, o, false, Xn);
-    load_row<P, kLayout, kVec2>(rows_rsrc(y, row_next, g.width, rows_next), C, l, o, false, Yn);
-    load_row<P, kLayout, kVec2>(rows_rsrc(gout, row_next, g.width, rows_next), C, l, o, true, Gn);
-#else
     if (it > 0) {
       load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
       load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
       load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
     }
-#endif
 
     float DX[P::kKeys][2], DY[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       DX[k][0] = DX[k][1] = DY[k][0] = DY[k][1] = 0.f;
     });
-#if !O2MI_BWD_WREG
     // Re-read the weights from LDS every iteration: hoisting the loop-invariant
     // reads out of the loop would cost as many registers.
     asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
-#endif
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
       constexpr bool freq3 = out_is_freq<P>(p);
-#if O2MI_BWD_WREG
-      const float wv = wreg[p];
-#else
       const float wv = staged_weight<P, kTile, p>(lds_w, col);
-#endif
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       dwacc[p] = fmaf(G[ps.k3][0], f0, dwacc[p]);
@@ -673,22 +541,10 @@ __global__ __launch_bounds__(kBlock, O2MI_BWD_WAVES) void tp_backward_kernel(
         }
       });
     }
-    store_row<P, kLayout, kVec2, O2MI_BWD_STORE_CPOL>(rows_rsrc(dx, row0, g.width, rows), C, l,
-                                                      ox, DX);
-    store_row<P, kLayout, kVec2, O2MI_BWD_STORE_CPOL>(rows_rsrc(dy, row0, g.width, rows), C, l,
-                                                      oy, DY);
-
-#if O2MI_BWD_PREFETCH
-    static_for<P::kKeys>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      X[k][0] = Xn[k][0];
-      X[k][1] = Xn[k][1];
-      Y[k][0] = Yn[k][0];
-      Y[k][1] = Yn[k][1];
-      G[k][0] = Gn[k][0];
-      G[k][1] = Gn[k][1];
-    });
-#endif
+    store_row<P, kLayout, kVec2, kBackwardStorePolicy>(rows_rsrc(dx, row0, g.width, rows), C, l,
+                                                       ox, DX);
+    store_row<P, kLayout, kVec2, kBackwardStorePolicy>(rows_rsrc(dy, row0, g.width, rows), C, l,
+                                                       oy, DY);
   }
 
   if ((needed & 4) && l.active) {

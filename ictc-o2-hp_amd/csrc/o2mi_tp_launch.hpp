@@ -58,11 +58,10 @@ hipError_t launch_forward(const float* x, const float* y, const float* w, float*
                           const TPGeom& g, int grid, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
-  const size_t lds = O2MI_FWD_WREG ? 0 : lds_bytes<P, kForwardTile>();
-  hipError_t err = allow_lds(kernel, lds, done);
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
-                     stream, x, y, w, out, g);
+  (void)kernel;
+  (void)done;
+  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), 0, stream,
+                     x, y, w, out, g);
   return hipGetLastError();
 }
 
@@ -72,10 +71,10 @@ hipError_t launch_backward(const float* x, const float* y, const float* w, const
                            int needed, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-  const size_t lds = O2MI_BWD_WREG ? 0 : lds_bytes<P, kBackwardTile>();
+  const size_t lds = lds_bytes<P, kBackwardTile>();
   hipError_t err = allow_lds(kernel, lds, done);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((tp_backward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), lds,
+  hipLaunchKernelGGL((tp_backward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBackwardBlock), lds,
                      stream, x, y, w, gout, dx, dy, partial, g, needed);
   return hipGetLastError();
 }
@@ -113,21 +112,17 @@ int occupancy_of(bool backward) {
   static std::atomic<uint64_t> done_f{0}, done_b{0};
   if (backward) {
     const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-    const size_t lds = O2MI_BWD_WREG ? 0 : lds_bytes<P, kBackwardTile>();
+    const size_t lds = lds_bytes<P, kBackwardTile>();
     if (allow_lds(kernel, lds, done_b) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
+            &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBackwardBlock, lds) != hipSuccess)
       return 1;
   } else {
-    const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
-    const size_t lds = O2MI_FWD_WREG ? 0 : lds_bytes<P, kForwardTile>();
-    if (allow_lds(kernel, lds, done_f) != hipSuccess) return 1;
+    (void)done_f;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, lds) != hipSuccess)
+            &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, 0) != hipSuccess)
       return 1;
   }
-  const int cap = backward ? O2MI_BWD_MAX_BLOCKS_PER_CU : O2MI_FWD_MAX_BLOCKS_PER_CU;
-  if (cap > 0 && blocks > cap) blocks = cap;
   return blocks > 0 ? blocks : 1;
 }
 

@@ -1,7 +1,7 @@
 // Host check of the TP kernels' row schedules (o2mi_tp.hpp row_schedule):
 // over many (rows, rows per iteration, blocks), in forward and reverse order,
 // every row is visited by exactly one (block, iteration) and every iteration
-// the kernels may address, including the prefetch of iteration `iters`, has a
+// a kernel may address, including one past the last (iteration `iters`), has a
 // descriptor inside [0, n_rows) or covers no rows.  Prints "<cases> cases,
 // <bad> bad" and exits non-zero on the first violation.
 #include <cstdio>
@@ -15,8 +15,6 @@ static int check(int64_t n, int rows_per_iter, int64_t groups) {
   g.n_rows = n;
   g.rows_per_iter = rows_per_iter;
   g.groups = groups;
-  const int64_t chunks = (n + rows_per_iter - 1) / rows_per_iter;
-  g.rows_per_group = ((chunks + groups - 1) / groups) * rows_per_iter;
   std::vector<int> seen(n, 0);
   for (int64_t b = 0; b < groups; ++b) {
     const o2mi::RowSchedule s = o2mi::row_schedule<kReverse>(g, b);
