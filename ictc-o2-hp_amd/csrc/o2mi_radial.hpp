@@ -54,7 +54,15 @@ struct REntry {
 struct RPath {
   int i, j, k;
   int mask;  // bit (c*4 + a*2 + b): coupling slot [out c][in1 a][in2 b] is non-zero
+  int neg;   // bit set: that slot's coupling is negative (all slots share one magnitude)
 };
+
+// Slot of the lowest non-zero coupling of a path.
+constexpr int first_slot(int mask) {
+  int s = 0;
+  while (s < 8 && !((mask >> s) & 1)) ++s;
+  return s;
+}
 
 using f4 = float __attribute__((ext_vector_type(4)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));

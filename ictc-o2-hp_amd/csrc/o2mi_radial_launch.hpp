@@ -5,6 +5,7 @@
 
 #include "o2mi_radial.hpp"
 #include "o2mi_radial_streamed.hpp"
+#include "o2mi_radial_weight.hpp"
 #include "o2mi_uvu_vshared.hpp"
 
 namespace o2mi {
@@ -76,7 +77,11 @@ hipError_t launch_backward(const Args& a, const float* gout, float* gx, float* g
 template <class Plan, int KH>
 hipError_t launch_weight(const Args& a, const float* gout, int64_t edges_per_slice, int slices,
                          float* part_alpha, float* part_bias, hipStream_t s) {
-  if constexpr (Plan::kWgtStreamed)
+  if constexpr (Plan::kWgtTwoPhase)
+    hipLaunchKernelGGL((radial_weight_gw_kernel<Plan, KH>),
+                       dim3((unsigned)slices, (unsigned)(a.C / 16)), dim3(kGwThreads), 0, s, a,
+                       gout, edges_per_slice, part_alpha, part_bias);
+  else if constexpr (Plan::kWgtStreamed)
     hipLaunchKernelGGL((radial_weight_streamed_kernel<Plan, KH>),
                        dim3((unsigned)slices, (unsigned)(a.C / 16), wgt_groups<Plan>()),
                        dim3(64 * kSWgtWaves), 0, s, a, gout, edges_per_slice, part_alpha,
@@ -170,7 +175,7 @@ const VSharedLaunchers* vshared_launchers() {
 
 template <class Plan>
 constexpr int weight_groups() {
-  if constexpr (Plan::kWgtStreamed) return wgt_groups<Plan>();
+  if constexpr (Plan::kWgtStreamed && !Plan::kWgtTwoPhase) return wgt_groups<Plan>();
   else return 1;
 }
 

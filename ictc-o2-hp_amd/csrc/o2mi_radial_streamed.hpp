@@ -575,7 +575,7 @@ constexpr bool wgt_uses(int q0, int n, int e) {
 }
 
 template <class Plan, int KH, int Q0, int NPW>
-__device__ __forceinline__ void wgt_step(const float* buf, const float* cf, int edge, int j,
+__device__ __forceinline__ void wgt_step(const float* buf, int edge, int j,
                                          f4 (&ga)[Plan::kWgtPaths][Geom<KH>::kTiles],
                                          float (&gb)[Plan::kWgtPaths]) {
   using G = Geom<KH>;
@@ -616,13 +616,20 @@ __device__ __forceinline__ void wgt_step(const float* buf, const float* cf, int 
     constexpr REntry X = Plan::e1[ps.i];
     constexpr REntry Y = Plan::e2[ps.j];
     constexpr REntry O = Plan::e1[ps.k];
+    // The path's weight adjoint divided by its coupling magnitude: the
+    // couplings' signs are compiled, the magnitude is applied once to the
+    // finished sums (wgt_body), so no coupling is read per step.
     float gw = 0.f;
-    const auto cfs = load_coefs<ps.mask>(cf, p);
     static_for<8>([&](auto sc) __attribute__((always_inline)) {
       constexpr int slot = decltype(sc)::value;
       constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-      if constexpr ((ps.mask >> slot) & 1)
-        gw += coef_at<slot>(cfs) * yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+      if constexpr ((ps.mask >> slot) & 1) {
+        const float t = yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+        if constexpr ((ps.neg >> slot) & 1)
+          gw -= t;
+        else
+          gw += t;
+      }
     });
     gb[q] += gw;
     static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
@@ -641,8 +648,9 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
   using T = WTile<Plan, KH, NT>;
   constexpr int P = Plan::kPaths;
   constexpr int kWeightEdges = Plan::kWeightEdges;
+  // The first kCoefPad floats of the block's LDS are not used by this kernel
+  // (its couplings are compiled signs and one magnitude per path).
   constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
-  float* s_coef = s_mem;
   float* s_tile = s_mem + kCoefPad;
 
   const int lane = threadIdx.x & 63;
@@ -653,7 +661,6 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
   const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
   const int tiles = end > begin ? (int)((end - begin + kWeightEdges - 1) / kWeightEdges) : 0;
 
-  for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_coef[idx] = a.coef[idx];
   f4 ga[Plan::kWgtPaths][G::kTiles];
   float gb[Plan::kWgtPaths];
   static_for<Plan::kWgtPaths>([&](auto qc) __attribute__((always_inline)) {
@@ -690,10 +697,7 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
         if (wave == w) {
 #pragma unroll
           for (int s = 0; s < kWeightEdges / 4; ++s) {
-            int coef_off = 0;
-            asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
-            const float* cf = s_coef + coef_off;
-            wgt_step<Plan, KH, q0, np>(buf, cf, 4 * s + g, j, ga, gb);
+            wgt_step<Plan, KH, q0, np>(buf, 4 * s + g, j, ga, gb);
           }
         }
       }
@@ -714,15 +718,17 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
         static_for<np>([&](auto qc) __attribute__((always_inline)) {
           constexpr int q = decltype(qc)::value;
           const int64_t row = (int64_t)Plan::wgt[q0 + q] * a.C + u0 + j;
+          constexpr int p = Plan::wgt[q0 + q];
+          const float mag = fabsf(a.coef[p * 8 + first_slot(Plan::paths[p].mask)]);
           static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {
             constexpr int tt = decltype(tc)::value;
             const int h = 16 * tt + 4 * g;
-            if (h < a.H) *reinterpret_cast<f4*>(pa + row * a.H + h) = ga[q][tt];
+            if (h < a.H) *reinterpret_cast<f4*>(pa + row * a.H + h) = ga[q][tt] * mag;
           });
           float b = gb[q];
           b += __shfl_xor(b, 16);
           b += __shfl_xor(b, 32);
-          if (g == 0) pb[row] = b;
+          if (g == 0) pb[row] = b * mag;
         });
       }
     }

@@ -118,7 +118,7 @@ def test_generated_orders_group_paths(tmp_path):
     text = text[text.index("struct R6f6c {"):]
     text = text[:text.index("\n};\n")]
     paths = [tuple(map(int, t)) for t in
-             re.findall(r"\{(\d+), (\d+), (\d+), \d+\}", text.split("paths[kPaths] = ")[1]
+             re.findall(r"\{(\d+), (\d+), (\d+), \d+, \d+\}", text.split("paths[kPaths] = ")[1]
                         .split(";")[0])]
     orders = {k: list(map(int, re.search(k + r"\[kPaths\] = \{([^}]*)\}", text)
                           .group(1).split(", "))) for k in ("fwd", "bwd", "wgt")}
@@ -208,3 +208,34 @@ def test_uvu_plan_create_validation():
                                           None, 0, 10, 7, None) == -2
     for h in (v1, v2):
         assert lib.o2mi_radial_plan_destroy(h) == 0
+
+
+def test_compiled_coupling_signs_hold_for_every_normalization(tmp_path):
+    """The fused kernels compile each path's non-zero coupling slots (mask) and
+    their signs (neg) and read one magnitude per path at run time.  For every
+    fused structure and every normalization the module's couplings must have
+    exactly those slots and signs, and one magnitude per path."""
+    import re
+    import build_native
+    from ictc_o2_hp.uvu_o2 import UvuLayout, uvu_plan
+    build_native.generate_radial(tmp_path)
+    text = (tmp_path / "o2mi_radial_plans.h").read_text()
+    for m, p1, m2, p2 in build_native.RADIAL_STRUCTURES:
+        name = build_native._radial_name(m, p1, m2, p2)
+        body = text[text.index(f"struct {name} {{"):]
+        body = body[:body.index("\n};\n")]
+        rows = [tuple(map(int, t)) for t in re.findall(
+            r"\{(\d+), (\d+), (\d+), (\d+), (\d+)\}", body.split("paths[kPaths] = ")[1].split(";")[0])]
+        first, second = UvuLayout.build(5, m, p1), UvuLayout.build(3, m2, p2)
+        for norm in ("component", "norm"):
+            for pnorm in ("none", "element", "path"):
+                paths, coef = uvu_plan(first.entries, second.entries, norm, pnorm, 3)
+                assert len(paths) == len(rows)
+                for (i, j, k), cg, (ri, rj, rk, mask, neg) in zip(paths, coef, rows):
+                    assert (i, j, k) == (ri, rj, rk)
+                    flat = cg.reshape(-1)     # slot = out * 4 + in1 * 2 + in2
+                    nz = np.abs(flat) > 1e-12
+                    assert sum(1 << s for s in range(8) if nz[s]) == mask
+                    assert sum(1 << s for s in range(8) if flat[s] < -1e-12) == neg
+                    mags = np.abs(flat[nz])
+                    assert np.allclose(mags, mags[0], rtol=1e-12)
