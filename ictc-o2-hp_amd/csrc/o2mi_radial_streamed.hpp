@@ -28,10 +28,7 @@ namespace radial {
 // accumulators and the next x entry), and still run 18% faster than at one
 // wave per SIMD with 512 registers.
 constexpr int kSFwdWaves = 8;
-#ifndef O2MI_SBWD_WAVES
-#define O2MI_SBWD_WAVES 8
-#endif
-constexpr int kSBwdWaves = O2MI_SBWD_WAVES;
+constexpr int kSBwdWaves = 8;
 
 template <class Plan, int KH>
 struct SLayout {
@@ -153,21 +150,16 @@ __device__ __forceinline__ void store_zero_entry(__amdgpu_buffer_rsrc_t r, uint3
 // memory.  The last two have no hidden, no bias and no matrix work.
 constexpr int kAffineW = 0, kSharedW = 1, kRowW = 2;
 
-#ifndef O2MI_ROW_AHEAD
-#define O2MI_ROW_AHEAD 2
-#endif
 // kRowW: a lane's weight loads run this many paths ahead of their use, in a
 // ring of registers refilled per channel tile (position q uses slot q mod
 // kRowAhead; the ring restarts at each tile, one load latency per tile).
-constexpr int kRowAhead = O2MI_ROW_AHEAD;
+constexpr int kRowAhead = 2;
 
 // kRowW: cache policy of the per-row weight-adjoint stores.  Default
 // (write-back) lets L2 merge the two halves of a 128-byte line that the two
 // waves of a pair write at about the same time; non-temporal 16-byte stores
 // (2) measured 10% slower.
-#ifndef O2MI_ROW_DW_POLICY
-#define O2MI_ROW_DW_POLICY 0
-#endif
+constexpr int kRowDwPolicy = 0;
 
 // Ring slot refill at traversal position q: the weights of position q +
 // kRowAhead of this channel tile.
@@ -239,6 +231,8 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
     chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   }
   f4 ring[kRowAhead];
+  constexpr int ND1 = dim1_before<Plan>(Plan::kEntries1);
+  float xcarry[4 * (ND1 > 0 ? ND1 : 1)] = {};
   int parity = 0;  // LDS buffer of the current chunk
   for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
     __syncthreads();
@@ -250,8 +244,10 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
     const int u = u0 + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, false>(ring, rw, wrow, a.C);
+    // kRowW: the two waves of a pair read both halves of a line already.
+    const TilePair tp = tile_pair(kMode != kRowW, u0, u_begin, u_end);
     float xv[4 * NC];
-    load_row<Plan>(rx, xsrc, a.C, u, xv);
+    load_row_paired<Plan>(rx, xsrc, a.C, u, xv, xcarry, tp);
     static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
       constexpr int e = decltype(ec)::value;
       constexpr REntry O = Plan::e1[e];
@@ -385,6 +381,13 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
     chunk_commit<Plan, KH, NT>(pf, s_mem + L::kBuf0);
   }
   f4 ring[kRowAhead];
+  constexpr int ND1 = dim1_before<Plan>(Plan::kEntries1);
+  // Tile pairing carries 4 registers per one-component entry for x and for
+  // g.  Taken where it costs no occupancy or spill: the affine mode with one
+  // such entry (canonical first input) and a small row state (m_max <= 4
+  // canonical, and m_max 5 canonical x canonical).
+  constexpr bool kPair = kMode == kAffineW && ND1 == 1 && 4 * NC + 2 * NY <= 72;
+  float gcarry[4 * (ND1 > 0 ? ND1 : 1)] = {}, xcarry[4 * (ND1 > 0 ? ND1 : 1)] = {};
   int parity = 0;
   for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
     __syncthreads();
@@ -396,8 +399,9 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
     const int u = u0 + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, true>(ring, rw, wrow, a.C);
+    const TilePair tp = tile_pair(kPair, u0, u_begin, u_end);
     float gv[4 * NC];
-    load_row<Plan>(rg, xrow, a.C, u, gv);
+    load_row_paired<Plan>(rg, xrow, a.C, u, gv, gcarry, tp);
     static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
       constexpr int e = decltype(ec)::value;
       constexpr REntry X = Plan::e1[e];
@@ -407,8 +411,10 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
     // group ahead of its use).
     float xc[8], xn[8], dxc[8];
     {
-      constexpr REntry X0 = Plan::e1[Plan::paths[Plan::bwd[0]].i];
-      load_entry<X0.dim>(rx, xsrc, X0.off * a.C, u, xn);
+      constexpr int i0 = Plan::paths[Plan::bwd[0]].i;
+      constexpr REntry X0 = Plan::e1[i0];
+      load_entry_paired<X0.dim>(rx, xsrc, X0.off * a.C, u, xn, xcarry + 4 * dim1_before<Plan>(i0),
+                                tp);
     }
     static_for<NCH>([&](auto cc) __attribute__((always_inline)) {
       constexpr int c = decltype(cc)::value;
@@ -449,8 +455,10 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
               return t;
             }();
             if constexpr (qn < P) {
-              constexpr REntry XN = Plan::e1[Plan::paths[Plan::bwd[qn]].i];
-              load_entry<XN.dim>(rx, xsrc, XN.off * a.C, u, xn);
+              constexpr int in = Plan::paths[Plan::bwd[qn]].i;
+              constexpr REntry XN = Plan::e1[in];
+              load_entry_paired<XN.dim>(rx, xsrc, XN.off * a.C, u, xn,
+                                        xcarry + 4 * dim1_before<Plan>(in), tp);
             }
           }
         }
@@ -489,7 +497,7 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
           if (need_w) {
             __builtin_amdgcn_raw_buffer_store_b128(
                 __builtin_bit_cast(u32x4, f4{gw[0], gw[1], gw[2], gw[3]}), rdw,
-                (int)(wrow + (uint32_t)(p * a.C) * 4u), 0, O2MI_ROW_DW_POLICY);
+                (int)(wrow + (uint32_t)(p * a.C) * 4u), 0, kRowDwPolicy);
           }
         }
         if constexpr (kMode == kAffineW) {

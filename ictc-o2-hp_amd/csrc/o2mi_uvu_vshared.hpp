@@ -26,13 +26,10 @@ namespace radial {
 
 constexpr int kVK = 8;  // copies of the second input a kernel covers (zero-padded)
 
-#ifndef O2MI_VCHUNK
-#define O2MI_VCHUNK 32
-#endif
 // Paths per staged weight chunk: a path costs only 2 MFMAs per second-input
 // component here, so chunks are deeper than the radial kernels' to amortise
 // the chunk barrier.
-constexpr int kVChunk = O2MI_VCHUNK;
+constexpr int kVChunk = 32;
 
 // Entry of the V = 1 second-input component c.
 template <class Plan>
