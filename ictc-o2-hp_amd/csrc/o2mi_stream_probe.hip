@@ -7,8 +7,9 @@
 // each thread loading its share of a chunk with 4-, 8- or 16-byte
 // non-temporal accesses, all loads of a chunk before its stores.  It sweeps
 // access width x rows per chunk (R = 1, 2, 4) x 1..8 blocks of 256 threads per
-// CU and reports the best GB/s of each mix (min of 5 timed launches per
-// configuration).  It measures what the memory system delivers for these
+// CU and reports the best configuration's GB/s for each mix, each
+// configuration timed as the median of 7 launches (a minimum let one launch
+// timed short set a ceiling 10% above every other reading).  It measures what the memory system delivers for these
 // mixes; the kernels are judged against it next to the 8 TB/s nominal peak.
 //
 // Usage: o2mi_stream_probe [rows] [width] [--table]
@@ -93,24 +94,29 @@ __global__ __launch_bounds__(kThreads) void r2w1(const T* __restrict__ x,
 }
 
 template <class F>
-float best_ms(F&& launch) {
+float median_ms(F&& launch) {
+  constexpr int kReps = 7;
   hipEvent_t e0, e1;
   PROBE_CHECK(hipEventCreate(&e0));
   PROBE_CHECK(hipEventCreate(&e1));
   launch();
-  float best = 1e30f;
-  for (int rep = 0; rep < 5; ++rep) {
+  float ms[kReps];
+  for (int rep = 0; rep < kReps; ++rep) {
     PROBE_CHECK(hipEventRecord(e0));
     launch();
     PROBE_CHECK(hipEventRecord(e1));
     PROBE_CHECK(hipEventSynchronize(e1));
-    float ms = 0.f;
-    PROBE_CHECK(hipEventElapsedTime(&ms, e0, e1));
-    if (ms < best) best = ms;
+    PROBE_CHECK(hipEventElapsedTime(&ms[rep], e0, e1));
   }
   PROBE_CHECK(hipEventDestroy(e0));
   PROBE_CHECK(hipEventDestroy(e1));
-  return best;
+  for (int i = 1; i < kReps; ++i)  // insertion sort of 7 values
+    for (int j = i; j > 0 && ms[j] < ms[j - 1]; --j) {
+      const float t = ms[j];
+      ms[j] = ms[j - 1];
+      ms[j - 1] = t;
+    }
+  return ms[kReps / 2];
 }
 
 struct Best {
@@ -138,11 +144,11 @@ void sweep(Sweep& s, int rows_per_chunk) {
   T* const* out = reinterpret_cast<T* const*>(s.buf);
   for (int per_cu : {1, 2, 3, 4, 6, 8}) {
     const int grid = per_cu * s.cus;
-    const float t3 = best_ms([&] {
+    const float t3 = median_ms([&] {
       hipLaunchKernelGGL((r3w2<T, PER>), dim3(grid), dim3(kThreads), 0, 0, in[0], in[1], in[2],
                          out[3], out[4], chunks, vecs, last_vecs);
     });
-    const float t2 = best_ms([&] {
+    const float t2 = median_ms([&] {
       hipLaunchKernelGGL((r2w1<T, PER>), dim3(grid), dim3(kThreads), 0, 0, in[0], in[1],
                          out[3], chunks, vecs, last_vecs);
     });
