@@ -1,5 +1,5 @@
 // Table-driven O(2) tensor-product kernels: any m_max, run when no plan is
-// compiled for the representation (the compiled plans cover m_max <= 6).
+// compiled for the representation (the compiled plans cover m_max <= 8).
 //
 // The path table is the op's own device metadata (triton_o2.py:786-794,
 // built as in runtime_weight.py:14-29): path_info int32 [P, 25] =

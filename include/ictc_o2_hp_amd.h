@@ -51,7 +51,7 @@ const char *o2mi_version(void);
  * normalization) with flat layout `layout`.  Replaces the per-module
  * metadata registration of triton_o2.py:1098-1132 (_METADATA / metadata_id)
  * and the layout override of triton_o2.py:1226-1234.  A plan may be shared
- * by threads.  Plans with m_max <= 6 have compiled kernels
+ * by threads.  Plans with m_max <= 8 have compiled kernels
  * (o2mi_tp_forward_f32 / o2mi_tp_backward_f32); larger m_max (up to 46 full,
  * 47 canonical) give table-driven plans, which only the *_tables_* entry
  * points run (the compiled ones return O2MI_ERR_UNSUPPORTED for them). */
@@ -105,7 +105,7 @@ int o2mi_tp_backward_f32(const o2mi_tp_plan *plan, const float *x, const float *
                          int64_t n_rows, int needed, void *stream);
 
 /* Table-driven forward for any plan, including plans without compiled
- * kernels (m_max >= 7; o2mi_tp_plan_create accepts m_max up to 46 in full
+ * kernels (m_max >= 9; o2mi_tp_plan_create accepts m_max up to 46 in full
  * parity, 47 in canonical).  Replaces the o2_forward op (triton_o2.py:786-875)
  * for plans the reference JIT-specialises (triton_o2.py:1098-1132): the path
  * table is the op's own device metadata, path_info int32 [n_paths, 25] and

@@ -146,16 +146,18 @@ def test_tp_ops_refuse_mismatched_shapes_before_launch(lib):
 
 
 def test_plans_beyond_compiled_orders_are_table_driven(lib):
-    """m_max >= 7 plans are created table-driven (width and P_w from the
-    selection rules, equal to the host plan); the key limit is 48."""
+    """Plans beyond the compiled orders (m_max >= 9) are created table-driven
+    (width and P_w from the selection rules, equal to the host plan); the key
+    limit is 48."""
     from ictc_o2_hp import _native
     from ictc_o2_hp.plan import TPPlan
     for c, m, parity in ((16, 7, "full"), (5, 8, "canonical"), (3, 10, "full"),
-                         (2, 46, "full"), (2, 47, "canonical"), (32, 6, "full")):
+                         (4, 9, "canonical"), (2, 46, "full"), (2, 47, "canonical"),
+                         (32, 6, "full")):
         native = _native.TPNativePlan(c, m, parity, "component", 0)
         host = TPPlan(c, m, parity)
         assert (native.width, native.weight_numel) == (host.width, host.weight_numel)
-        assert native.compiled == (m <= 6)
+        assert native.compiled == (m <= 8)
     for m, parity in ((47, 1), (48, 0)):
         handle = ctypes.c_void_p()
         assert lib.o2mi_tp_plan_create(2, m, parity, 0, 0, ctypes.byref(handle)) == -2

@@ -359,23 +359,32 @@ def test_component_major_matches_reference_layout_vectors():
             assert O.normalized_error(data[f"{name}/{key}"], value) <= TOL, (name, key)
 
 
-# m_max beyond the compiled plans: the table-driven kernels, which read the
-# module's path_info / path_coefficients tables (the reference JIT-specialises
-# any m_max, triton_o2.py:1098-1132).
-TABLE_DRIVEN = [
+# m_max above the benchmark grid: compiled plans up to m8 (m8 full has 136
+# paths), beyond that the table-driven kernels, which read the module's
+# path_info / path_coefficients tables (the reference JIT-specialises any
+# m_max, triton_o2.py:1098-1132).
+HIGH_ORDER = [
     # C, M, parity, normalization, N, layout class
     (16, 7, "full", "component", 300, None),
     (16, 8, "canonical", "component", 257, None),
+    (12, 8, "full", "norm", 130, None),
     (5, 7, "canonical", "norm", 40, None),           # odd C
-    (9, 10, "full", "norm", 33, None),
     (24, 7, "full", "component", 64, "component_major"),
+    (6, 8, "canonical", "norm", 33, "component_major"),
+    # table-driven
+    (9, 10, "full", "norm", 33, None),
+    (16, 9, "canonical", "component", 129, None),
+    (8, 9, "full", "component", 70, None),
     (7, 9, "canonical", "component", 50, "component_major"),
+    (4, 10, "full", "norm", 20, "component_major"),
 ]
 
 
-@pytest.mark.parametrize("channels,m_max,parity,normalization,n_rows,layout", TABLE_DRIVEN)
-def test_table_driven_plans_match_oracle(channels, m_max, parity, normalization, n_rows, layout):
+@pytest.mark.parametrize("channels,m_max,parity,normalization,n_rows,layout", HIGH_ORDER)
+def test_high_order_plans_match_oracle(channels, m_max, parity, normalization, n_rows, layout):
     from ictc_o2_hp import ComponentMajorTensorProduct
+    print(f"case high order C{channels} m{m_max} {parity} {normalization} N{n_rows} "
+          f"layout {layout}", flush=True)
     rng = np.random.default_rng(700 + channels + m_max)
     plan = O.OraclePlan(channels, m_max, parity, normalization)
     cls = ComponentMajorTensorProduct if layout else None
@@ -386,12 +395,15 @@ def test_table_driven_plans_match_oracle(channels, m_max, parity, normalization,
     _check(plan, module, x, y, g, layout=lay)
 
 
-def test_table_driven_rows_at_scale():
-    """m7 full C32 at N = 65536 (many row groups of the weight adjoint): 256
-    random rows against the oracle, dw from a cotangent masked to them."""
-    rng = np.random.default_rng(7007)
-    plan = O.OraclePlan(32, 7, "full")
-    module = _module(32, 7, "full")
+@pytest.mark.parametrize("channels,m_max,parity", [(32, 8, "full"), (32, 9, "canonical")])
+def test_high_order_rows_at_scale(channels, m_max, parity):
+    """N = 65536 (many blocks and row groups; compiled m8 full, table-driven
+    m9): 256 random rows against the oracle, dw from a cotangent masked to
+    them."""
+    print(f"case high order at scale C{channels} m{m_max} {parity}", flush=True)
+    rng = np.random.default_rng(7007 + m_max)
+    plan = O.OraclePlan(channels, m_max, parity)
+    module = _module(channels, m_max, parity)
     n = 65536
     x, y, g = (rng.standard_normal((n, plan.width)) for _ in range(3))
     rows = np.sort(rng.choice(n, 256, replace=False))
@@ -399,6 +411,8 @@ def test_table_driven_rows_at_scale():
 
 
 @pytest.mark.parametrize("channels,m_max,parity,normalization,layout", [
+    (16, 8, "full", "component", 0),
+    (10, 7, "canonical", "norm", 1),
     (32, 6, "full", "component", 0),
     (17, 3, "full", "norm", 0),
     (5, 4, "canonical", "component", 1),
@@ -444,7 +458,9 @@ def test_table_driven_kernels_match_compiled_kernels(channels, m_max, parity, no
 def test_table_driven_backward_roles_and_reproducible():
     """Role subsets of the table-driven backward and bitwise repeatable dw."""
     torch.manual_seed(3)
-    module = _module(8, 7, "full")
+    from ictc_o2_hp import _native
+    assert not _native.TPNativePlan(8, 9, "full", "component", 0).compiled
+    module = _module(8, 9, "full")
     gen = torch.Generator(device="cuda").manual_seed(8)
     x = torch.randn((500, module.representation_dimension), device="cuda", generator=gen)
     y = torch.randn(x.shape, device="cuda", generator=gen)
