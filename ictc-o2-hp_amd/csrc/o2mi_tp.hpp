@@ -63,8 +63,11 @@ struct TermSpec {
 // row is touched once per kernel, so loads are non-temporal; the forward's
 // stores are non-temporal + sc1, the backward's non-temporal (measured best
 // at the headline shape: forward 0.938 -> 0.890 ms, backward 1.722 -> 1.659
-// ms together with the reverse row order of the backward).
-constexpr int kLoadPolicy = 2;
+// ms together with the reverse row order of the backward).  Default
+// (allocating) loads measured slower in either kernel (forward +3.6%,
+// backward +2.5%).
+constexpr int kForwardLoadPolicy = 2;
+constexpr int kBackwardLoadPolicy = 2;
 constexpr int kForwardStorePolicy = 18;
 constexpr int kBackwardStorePolicy = 2;
 
@@ -159,9 +162,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, i
                                            rows * width * 4, kRsrcFlags);
 }
 
+template <int kCpol>
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
   return __builtin_bit_cast(float,
-                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, kLoadPolicy));
+                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, kCpol));
 }
 
 using f32x2 = float __attribute__((ext_vector_type(2)));
@@ -169,10 +173,11 @@ using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 
 // Whole-vector bit casts only: hipcc 7.2 miscompiles __builtin_bit_cast of a
 // single vector element (both elements read as element 0).
+template <int kCpol>
 __device__ __forceinline__ void bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff,
                                        float& a, float& b) {
   const f32x2 v = __builtin_bit_cast(
-      f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, kLoadPolicy));
+      f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, soff, kCpol));
   a = v.x;
   b = v.y;
 }
@@ -200,24 +205,24 @@ __device__ __forceinline__ float pair_swap(float v) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
 }
 
-template <class P, int kLayout, bool kVec2, int K>
+template <class P, int kLayout, bool kVec2, int K, int kCpol>
 __device__ __forceinline__ void load_key(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
                                          uint32_t voff, float& v0, float& v1) {
   constexpr KeySpec ks = P::keys[K];
   const int soff = ks.off * C * 4;
   if constexpr (ks.dim == 1) {
-    v0 = bload(r, voff, soff);
+    v0 = bload<kCpol>(r, voff, soff);
     v1 = 0.f;
   } else {
     float a0, a1;
     if constexpr (kLayout == 0 && kVec2) {
-      bload2(r, voff, soff, a0, a1);
+      bload2<kCpol>(r, voff, soff, a0, a1);
     } else if constexpr (kLayout == 0) {
-      a0 = bload(r, voff, soff);
-      a1 = bload(r, voff + 4u, soff);
+      a0 = bload<kCpol>(r, voff, soff);
+      a1 = bload<kCpol>(r, voff + 4u, soff);
     } else {
-      a0 = bload(r, voff, soff);
-      a1 = bload(r, voff, soff + C * 4);
+      a0 = bload<kCpol>(r, voff, soff);
+      a1 = bload<kCpol>(r, voff, soff + C * 4);
     }
     if constexpr (P::kFull) {
       const bool odd = l.q != 0;
@@ -257,7 +262,7 @@ __device__ __forceinline__ void store_key(__amdgpu_buffer_rsrc_t r, int C, const
 }
 
 // Loads every key of one row set: x and y, and optionally the cotangent.
-template <class P, int kLayout, bool kVec2>
+template <class P, int kLayout, bool kVec2, int kCpol>
 __device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, int C, const Lane& l,
                                          const LaneOffsets& o, bool copy0_scalars,
                                          float (&V)[P::kKeys][2]) {
@@ -265,7 +270,7 @@ __device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, int C, const 
     constexpr int k = decltype(kc)::value;
     const uint32_t voff =
         P::keys[k].dim == 1 ? (copy0_scalars ? o.scalar_own : o.scalar) : o.freq;
-    load_key<P, kLayout, kVec2, k>(r, C, l, voff, V[k][0], V[k][1]);
+    load_key<P, kLayout, kVec2, k, kCpol>(r, C, l, voff, V[k][0], V[k][1]);
   });
 }
 
@@ -432,8 +437,10 @@ __global__ __launch_bounds__(kBlock, kForwardWaves) void tp_forward_kernel(
   for (int it = 0; it < sched.iters; ++it) {
     const int64_t row0 = sched.row0(it);
     const int rows = sched.rows(it);
-    load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
-    load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
+    load_row<P, kLayout, kVec2, kForwardLoadPolicy>(rows_rsrc(x, row0, g.width, rows), C, l, o,
+                                                    false, X);
+    load_row<P, kLayout, kVec2, kForwardLoadPolicy>(rows_rsrc(y, row0, g.width, rows), C, l, o,
+                                                    false, Y);
     float A[P::kKeys][2];
     static_for<P::kKeys>([&](auto kc) {
       A[decltype(kc)::value][0] = 0.f;
@@ -494,17 +501,23 @@ __global__ __launch_bounds__(kBackwardBlock, kBackwardWaves) void tp_backward_ke
   {
     const int64_t row0 = sched.row0(0);
     const int rows = sched.rows(0);
-    load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
-    load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
-    load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
+    load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(x, row0, g.width, rows), C, l, o,
+                                                     false, X);
+    load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(y, row0, g.width, rows), C, l, o,
+                                                     false, Y);
+    load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(gout, row0, g.width, rows), C, l,
+                                                     o, true, G);
   }
   for (int it = 0; it < sched.iters; ++it) {
     const int64_t row0 = sched.row0(it);
     const int rows = sched.rows(it);
     if (it > 0) {
-      load_row<P, kLayout, kVec2>(rows_rsrc(x, row0, g.width, rows), C, l, o, false, X);
-      load_row<P, kLayout, kVec2>(rows_rsrc(y, row0, g.width, rows), C, l, o, false, Y);
-      load_row<P, kLayout, kVec2>(rows_rsrc(gout, row0, g.width, rows), C, l, o, true, G);
+      load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(x, row0, g.width, rows), C, l,
+                                                       o, false, X);
+      load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(y, row0, g.width, rows), C, l,
+                                                       o, false, Y);
+      load_row<P, kLayout, kVec2, kBackwardLoadPolicy>(rows_rsrc(gout, row0, g.width, rows), C,
+                                                       l, o, true, G);
     }
 
     float DX[P::kKeys][2], DY[P::kKeys][2];
