@@ -244,7 +244,7 @@ BackwardShape backward_shape_for(const o2mi_tp_plan* p, int64_t n_rows, int vari
                                  int64_t target) {
   BackwardShape s{};
   s.variant = variant;
-  s.geom = geometry(p, n_rows, target, o2mi::kBackwardBlock, o2mi::kBackwardTile, &s.grid);
+  s.geom = geometry(p, n_rows, target, o2mi::kBackwardBlock, p->set->backward_tile, &s.grid);
   s.partial_rows = (int64_t)(s.grid / s.geom.tiles) * s.geom.rows_per_iter;
   s.splits = reduce_splits(s.partial_rows);
   const int64_t floats = (s.partial_rows + (s.splits > 1 ? s.splits : 0)) * p->weight_numel;
@@ -613,7 +613,7 @@ int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward,
   const o2mi::TPGeom geom =
       geometry(plan, n_rows, (int64_t)per_cu * device_cus(),
                backward ? o2mi::kBackwardBlock : o2mi::kBlock,
-               backward ? o2mi::kBackwardTile : o2mi::kForwardTile, &g);
+               backward ? plan->set->backward_tile : o2mi::kForwardTile, &g);
   if (grid) *grid = g;
   if (blocks_per_cu) *blocks_per_cu = per_cu;
   if (rows_per_iter) *rows_per_iter = geom.rows_per_iter;

@@ -80,12 +80,9 @@ constexpr int kBackwardStorePolicy = 2;
 constexpr int kBlock = 256;
 constexpr int kBackwardBlock = 256;  // 512 (two rows per iteration, one block per CU): same time
 constexpr int kForwardTile = 256;
-constexpr int kBackwardTile = 256;
 constexpr int kForwardWaves = 1;   // minimum waves per SIMD requested
 constexpr int kBackwardWaves = 2;
 static_assert(kForwardTile % 2 == 0 && kForwardTile <= kBlock, "tile must be even, <= block");
-static_assert(kBackwardTile % 2 == 0 && kBackwardTile <= kBackwardBlock,
-              "tile must be even, <= block");
 // Byte offset given to lanes with nothing to load or store: beyond any
 // descriptor size used here (< 2^31), with room to add key offsets.
 constexpr uint32_t kIdle = 0x80000000u;
@@ -324,6 +321,16 @@ constexpr size_t lds_bytes() {
   return sizeof(float) * (size_t)P::kUnits * (size_t)lds_unit<P, kTile>();
 }
 
+// Lanes of a row one backward block covers (backward_tile<P>() below): 256,
+// or 128 where a 256-lane stage of the path weights would need more than
+// 80 KiB of LDS (m7 full and larger plans), so that two blocks still share a
+// CU (the backward runs at two waves per SIMD).
+template <class P>
+constexpr int backward_tile() {
+  return lds_bytes<P, 256>() > 80 * 1024 ? 128 : 256;
+}
+static_assert(128 <= kBackwardBlock && 256 <= kBackwardBlock, "tiles must fit a block");
+
 template <class P, int kTile>
 __device__ __forceinline__ void stage_weights(float* lds, const float* __restrict__ w, int C,
                                               int tile) {
@@ -470,7 +477,7 @@ __global__ __launch_bounds__(kBackwardBlock, kBackwardWaves) void tp_backward_ke
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ gout, float* __restrict__ dx, float* __restrict__ dy,
     float* __restrict__ partial, TPGeom g, int needed) {
-  constexpr int kTile = kBackwardTile;
+  constexpr int kTile = backward_tile<P>();
   extern __shared__ float lds_w[];
   const int tile = blockIdx.x % g.tiles;
   const int64_t group = blockIdx.x / g.tiles;

@@ -38,6 +38,7 @@ struct TPKernelSet {
   TPForwardFn forward;
   TPBackwardFn backward;
   TPOccupancyFn blocks_per_cu;
+  int backward_tile;  // lanes of a row per backward block (backward_tile<P>())
 };
 
 // Sets the dynamic-LDS limit of `kernel` once per device (the backward uses
@@ -71,7 +72,7 @@ hipError_t launch_backward(const float* x, const float* y, const float* w, const
                            int needed, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-  const size_t lds = lds_bytes<P, kBackwardTile>();
+  const size_t lds = lds_bytes<P, backward_tile<P>()>();
   hipError_t err = allow_lds(kernel, lds, done);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((tp_backward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBackwardBlock), lds,
@@ -112,7 +113,7 @@ int occupancy_of(bool backward) {
   static std::atomic<uint64_t> done_f{0}, done_b{0};
   if (backward) {
     const void* kernel = reinterpret_cast<const void*>(&tp_backward_kernel<P, kLayout, kVec2>);
-    const size_t lds = lds_bytes<P, kBackwardTile>();
+    const size_t lds = lds_bytes<P, backward_tile<P>()>();
     if (allow_lds(kernel, lds, done_b) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBackwardBlock, lds) != hipSuccess)
@@ -146,6 +147,7 @@ const TPKernelSet* tp_kernel_set() {
       &forward_dispatch<P>,
       &backward_dispatch<P>,
       &occupancy_dispatch<P>,
+      backward_tile<P>(),
   };
   return &set;
 }

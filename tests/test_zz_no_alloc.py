@@ -50,6 +50,7 @@ def _both(plan, x, y, w, g, needed):
     (32, 2, "canonical", (40000, 77)),
     (17, 3, "full", (5000, 1)),
     (256, 4, "canonical", (9000, 640)),
+    (128, 8, "full", (20000, 333)),       # 128-lane backward tiles; grid cut to the scratch
 ])
 def test_noalloc_backward_matches_workspace_backward(channels, m_max, parity, rows):
     from ictc_o2_hp import _native
