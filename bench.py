@@ -62,6 +62,8 @@ def _args():
                    help="radial-grid: only this 'edges,channels' point (e.g. 131072,64)")
     p.add_argument("--grid-set", default="configs2", choices=("configs2", "all"),
                    help="grid: BASELINE.json configs[2] (96 points) or every published point (240)")
+    p.add_argument("--grid-rows", default=None,
+                   help="grid: only these row counts (comma-separated), e.g. 16384,32768")
     p.add_argument("--copy-probe", action="store_true",
                    help="after the run, copy 512 MiB 3 times with an elementwise kernel "
                         "(reference traffic for HBM counter calibration)")
@@ -673,6 +675,9 @@ def grid_main(args):
     if args.grid_set == "configs2":
         a100 = {k: v for k, v in a100.items() if k[1] in (32, 64, 128, 256) and k[2] in (1, 4, 6)}
     points = sorted(a100) + [(6400, 128, 6, "full")]
+    if args.grid_rows:
+        keep = {int(v) for v in args.grid_rows.split(",")}
+        points = [pt for pt in points if pt[0] in keep]
     records = []
     for n, c, m, parity in points:
         torch.manual_seed(34527)
