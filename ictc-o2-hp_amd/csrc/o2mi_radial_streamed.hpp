@@ -270,7 +270,15 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
       int arow_off = buf + L::kAlpha + j * G::kRow + KH * g, wsh_off = L::kBuf0 + 4 * g;
       asm volatile("" : "+v"(coef_off), "+v"(bias_off), "+v"(arow_off), "+v"(wsh_off));
       const float* cf = s_mem + coef_off;
-      static_for<(P - c * PC < PC ? P - c * PC : PC)>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int kCount = (P - c * PC < PC ? P - c * PC : PC);
+      // Next path's weight tile generated beside this path's products, as in
+      // the input adjoints, where the forward already holds more than 128
+      // registers (one block of two waves per SIMD either way); small rows
+      // (4 kComps1 + kComps2 <= 45) keep 128 and two blocks per CU instead.
+      constexpr bool kPipe = kMode == kAffineW && 4 * NC + Plan::kComps2 > 45;
+      f4 wn;
+      if constexpr (kPipe) wn = weight_tile<KH>(s_mem, bias_off, arow_off, 0, hid);
+      static_for<kCount>([&](auto sc) __attribute__((always_inline)) {
         constexpr int slot = decltype(sc)::value;
         constexpr int q = c * PC + slot;
         constexpr int p = Plan::fwd[q];
@@ -287,7 +295,13 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
           w = ring[q % kRowAhead];
           row_refill<Plan, false, q>(ring, rw, wrow, a.C);
         }
-        else w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        else if constexpr (kPipe) {
+          w = wn;
+          if constexpr (slot + 1 < kCount)
+            wn = weight_tile<KH>(s_mem, bias_off, arow_off, slot + 1, hid);
+        } else {
+          w = weight_tile<KH>(s_mem, bias_off, arow_off, slot, hid);
+        }
         const auto cfs = load_coefs<ps.mask>(cf, p);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
