@@ -593,7 +593,7 @@ int o2mi_tp_forward_f32(const o2mi_tp_plan* plan, const float* x, const float* y
   const int64_t target = (int64_t)plan->set->blocks_per_cu(variant, false) * device_cus();
   int grid = 0;
   const o2mi::TPGeom g =
-      geometry(plan, n_rows, target, o2mi::kBlock, o2mi::kForwardTile, &grid);
+      geometry(plan, n_rows, target, plan->set->forward_block, plan->set->forward_tile, &grid);
   O2miTimed timed;
   const bool timing = o2mi_timing_begin(s, &timed, O2MI_TIMED_TP_FORWARD);
   const hipError_t err = plan->set->forward(variant, x, y, w, out, g, grid, s);
@@ -612,8 +612,8 @@ int o2mi_tp_launch_shape(const o2mi_tp_plan* plan, int64_t n_rows, int backward,
   int g = 0;
   const o2mi::TPGeom geom =
       geometry(plan, n_rows, (int64_t)per_cu * device_cus(),
-               backward ? o2mi::kBackwardBlock : o2mi::kBlock,
-               backward ? plan->set->backward_tile : o2mi::kForwardTile, &g);
+               backward ? o2mi::kBackwardBlock : plan->set->forward_block,
+               backward ? plan->set->backward_tile : plan->set->forward_tile, &g);
   if (grid) *grid = g;
   if (blocks_per_cu) *blocks_per_cu = per_cu;
   if (rows_per_iter) *rows_per_iter = geom.rows_per_iter;

@@ -331,6 +331,25 @@ constexpr int backward_tile() {
 }
 static_assert(128 <= kBackwardBlock && 256 <= kBackwardBlock, "tiles must fit a block");
 
+// The forward keeps a lane's path weights in registers; with more than 100
+// paths in full parity (m7, m8) those registers leave 3 waves per SIMD at
+// one row per 4-wave iteration, and the kernel runs latency-bound (3.6 TB/s).
+// Those plans stage the weights in LDS like the backward instead, with
+// 128-lane tiles and 512-thread blocks (4 rows per iteration), so that LDS,
+// not registers, sets the occupancy (6 waves per SIMD at m7 full).
+template <class P>
+constexpr bool forward_lds() {
+  return P::kFull && P::kPaths > 100;
+}
+template <class P>
+constexpr int forward_block() {
+  return forward_lds<P>() ? 512 : kBlock;
+}
+template <class P>
+constexpr int forward_tile() {
+  return forward_lds<P>() ? 128 : kForwardTile;
+}
+
 template <class P, int kTile>
 __device__ __forceinline__ void stage_weights(float* lds, const float* __restrict__ w, int C,
                                               int tile) {
@@ -421,23 +440,33 @@ __host__ __device__ __forceinline__ RowSchedule row_schedule(const TPGeom& g, in
 // ---------------------------------------------------------------------------
 // Forward: out = sum over paths of w * CG(x, y)  (native_o2.py:209-221).
 template <class P, int kLayout, bool kVec2>
-__global__ __launch_bounds__(kBlock, kForwardWaves) void tp_forward_kernel(
+__global__ __launch_bounds__(forward_block<P>(), kForwardWaves) void tp_forward_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     float* __restrict__ out, TPGeom g) {
-  constexpr int kTile = kForwardTile;
+  constexpr int kTile = forward_tile<P>();
+  constexpr bool kLds = forward_lds<P>();
+  extern __shared__ float lds_w[];
   const int tile = blockIdx.x % g.tiles;
   const int64_t group = blockIdx.x / g.tiles;
   const Lane l = make_lane<P::kFull, kTile>(g, tile);
   const LaneOffsets o = lane_offsets<P::kFull, kLayout>(g, l);
   const int C = g.channels;
-  // This lane's weight of every path (times the coupling magnitude).
-  float wreg[P::kPaths];
-  static_for<P::kPaths>([&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    constexpr PathSpec ps = P::paths[p];
-    const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
-    wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
-  });
+  // This lane's weight of every path (times the coupling magnitude): in
+  // registers, or staged in LDS for the block's lanes (forward_lds).
+  float wreg[kLds ? 1 : P::kPaths];
+  WeightColumns<P> col{};
+  if constexpr (kLds) {
+    stage_weights<P, kTile>(lds_w, w, C, tile);
+    __syncthreads();
+    col = weight_columns<P>(l);
+  } else {
+    static_for<P::kPaths>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr PathSpec ps = P::paths[p];
+      const int unit = (P::kFull && out_is_freq<P>(p)) ? ps.wunits + l.q : ps.wunits;
+      wreg[p] = l.active ? w[unit * C + l.c] * ps.mag : 0.f;
+    });
+  }
 
   const RowSchedule sched = row_schedule<false>(g, group);
   float X[P::kKeys][2], Y[P::kKeys][2];
@@ -453,10 +482,13 @@ __global__ __launch_bounds__(kBlock, kForwardWaves) void tp_forward_kernel(
       A[decltype(kc)::value][0] = 0.f;
       A[decltype(kc)::value][1] = 0.f;
     });
+    if constexpr (kLds) asm volatile("" : "+v"(col.freq), "+v"(col.scalar));
     static_for<P::kPaths>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       constexpr PathSpec ps = P::paths[p];
-      const float wv = wreg[p];
+      float wv;
+      if constexpr (kLds) wv = staged_weight<P, kTile, p>(lds_w, col);
+      else wv = wreg[p];
       float f0, f1;
       path_value<P, p>(X, Y, f0, f1);
       A[ps.k3][0] = fmaf(wv, f0, A[ps.k3][0]);

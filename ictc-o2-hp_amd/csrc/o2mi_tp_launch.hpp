@@ -39,6 +39,8 @@ struct TPKernelSet {
   TPBackwardFn backward;
   TPOccupancyFn blocks_per_cu;
   int backward_tile;  // lanes of a row per backward block (backward_tile<P>())
+  int forward_block;  // threads per forward block (forward_block<P>())
+  int forward_tile;   // lanes of a row per forward block (forward_tile<P>())
 };
 
 // Sets the dynamic-LDS limit of `kernel` once per device (the backward uses
@@ -59,10 +61,13 @@ hipError_t launch_forward(const float* x, const float* y, const float* w, float*
                           const TPGeom& g, int grid, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
-  (void)kernel;
-  (void)done;
-  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(kBlock), 0, stream,
-                     x, y, w, out, g);
+  const size_t lds = forward_lds<P>() ? lds_bytes<P, forward_tile<P>()>() : 0;
+  if (lds > 0) {
+    const hipError_t err = allow_lds(kernel, lds, done);
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL((tp_forward_kernel<P, kLayout, kVec2>), dim3(grid), dim3(forward_block<P>()),
+                     lds, stream, x, y, w, out, g);
   return hipGetLastError();
 }
 
@@ -119,9 +124,11 @@ int occupancy_of(bool backward) {
             &blocks, tp_backward_kernel<P, kLayout, kVec2>, kBackwardBlock, lds) != hipSuccess)
       return 1;
   } else {
-    (void)done_f;
+    const void* kernel = reinterpret_cast<const void*>(&tp_forward_kernel<P, kLayout, kVec2>);
+    const size_t lds = forward_lds<P>() ? lds_bytes<P, forward_tile<P>()>() : 0;
+    if (lds > 0 && allow_lds(kernel, lds, done_f) != hipSuccess) return 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, tp_forward_kernel<P, kLayout, kVec2>, kBlock, 0) != hipSuccess)
+            &blocks, tp_forward_kernel<P, kLayout, kVec2>, forward_block<P>(), lds) != hipSuccess)
       return 1;
   }
   return blocks > 0 ? blocks : 1;
@@ -148,6 +155,8 @@ const TPKernelSet* tp_kernel_set() {
       &backward_dispatch<P>,
       &occupancy_dispatch<P>,
       backward_tile<P>(),
+      forward_block<P>(),
+      forward_tile<P>(),
   };
   return &set;
 }
