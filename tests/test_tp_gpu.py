@@ -371,6 +371,12 @@ HIGH_ORDER = [
     (5, 7, "canonical", "norm", 40, None),           # odd C
     (24, 7, "full", "component", 64, "component_major"),
     (6, 8, "canonical", "norm", 33, "component_major"),
+    # several 128-lane tiles per row (LDS-staged forward weights, 128-lane
+    # backward tiles), the last one partial
+    (80, 7, "full", "component", 70, None),
+    (128, 8, "full", "norm", 37, None),
+    (72, 7, "full", "component", 21, "component_major"),
+    (200, 8, "canonical", "component", 45, None),
     # table-driven
     (9, 10, "full", "norm", 33, None),
     (16, 9, "canonical", "component", 129, None),
