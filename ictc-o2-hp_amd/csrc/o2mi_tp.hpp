@@ -74,9 +74,11 @@ constexpr int kBackwardStorePolicy = 2;
 // Threads per block and the lanes of one row a block covers (a row of more
 // lanes is split over several blocks, "tiles").  The forward keeps each
 // lane's path weights in registers for the whole persistent kernel and runs
-// at up to 3 waves per SIMD; the backward holds one weight-adjoint
+// at up to 3 waves per SIMD (plans with many paths stage them in LDS
+// instead: forward_lds below); the backward holds one weight-adjoint
 // accumulator per path and lane in registers and needs 2 waves per SIMD to
-// hide its dependent FMA chains and LDS weight reads.
+// hide its dependent FMA chains and LDS weight reads.  These are the defaults;
+// forward_block, forward_tile and backward_tile below pick per plan.
 constexpr int kBlock = 256;
 constexpr int kBackwardBlock = 256;  // 512 (two rows per iteration, one block per CU): same time
 constexpr int kForwardTile = 256;
