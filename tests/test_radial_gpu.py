@@ -178,6 +178,62 @@ def test_streamed_channel_split_matches_unsplit():
         assert normalized_error(r, a[rows].double().cpu().numpy()) <= TOL
 
 
+# The streamed kernels read the 16-channel tiles of a block in pairs (the
+# one-component entries of the second tile carried from the first tile's
+# loads).  40,000 edges (313 blocks) run unsplit: C / 32 pairs plus a single
+# tile when C % 32 == 16.  The slices 20,000 and 18,000 (157 and 141 blocks)
+# split the channels in two 32-channel spans (a pair each, or a pair and a
+# single tile for C = 48); 2,000 edges (16 blocks) split them into single
+# tiles.  The pairing changes loads only, so output and dx agree bitwise.
+PAIRED = [
+    (48, 4, "canonical", "canonical", 64, {}),            # configs[4] structure at C = 48
+    (64, 3, "full", "full", 32, {}),                      # two one-component entries
+    (48, 6, "full", "canonical", 64, {"normalization": "norm"}),   # 254 paths
+    (32, 2, "canonical", "full", 16, {"path_normalization": "path"}),
+]
+
+
+@pytest.mark.parametrize("c,m,parity,parity_in2,hidden,kw", PAIRED)
+def test_paired_tiles_match_split_launches(c, m, parity, parity_in2, hidden, kw):
+    from ictc_o2_hp import radial_ops
+    tp, linear, module, plan = _build(c, m, parity, parity_in2, hidden, True, c + m, **kw)
+    assert radial_ops.fused_plan(tp._kernel_metadata_id, hidden) is not None
+    n = 40000
+    print(f"case paired tiles C={c} m={m} {parity}/{parity_in2} H={hidden} n={n}", flush=True)
+    torch.manual_seed(c + m)
+    x = torch.randn(n, tp.input1_dimension, device="cuda", requires_grad=True)
+    y = torch.randn(n, tp.input2_dimension, device="cuda", requires_grad=True)
+    h = torch.randn(n, hidden, device="cuda", requires_grad=True)
+    g = torch.randn(n, tp.input1_dimension, device="cuda")
+    params = (x, y, h, linear.weight, linear.bias)
+    out = module(x, y, h)
+    whole = torch.autograd.grad(out, params, g)
+    parts = []
+    for lo, hi in ((0, 20000), (20000, 22000), (22000, n)):
+        xs, ys, hs = (t.detach()[lo:hi].clone().requires_grad_() for t in (x, y, h))
+        o = module(xs, ys, hs)
+        parts.append((o,) + torch.autograd.grad(o, (xs, ys, hs, linear.weight, linear.bias),
+                                                g[lo:hi]))
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), torch.cat([p[0] for p in parts]))
+    assert torch.equal(whole[0], torch.cat([p[1] for p in parts]))
+    for k in (1, 2):   # dy, dhidden: split partial sums, another summation order
+        cat = torch.cat([p[k + 1] for p in parts]).double().cpu().numpy()
+        assert normalized_error(whole[k].double().cpu().numpy(), cat) <= TOL
+    for k in (3, 4):   # dalpha, dbias: linear in the rows
+        total = sum(p[k + 1] for p in parts).double().cpu().numpy()
+        assert normalized_error(total, whole[k].double().cpu().numpy()) <= TOL
+    rows = np.random.default_rng(c + m).choice(n, 32, replace=False)
+    alpha = linear.weight.detach().double().cpu().numpy()
+    b = linear.bias.detach().double().cpu().numpy()
+    xs, ys, hs, gs = (t.detach()[rows].double().cpu().numpy() for t in (x, y, h, g))
+    ref_out = U.radial_forward(plan, xs, ys, hs, alpha, b)
+    assert normalized_error(ref_out, out.detach()[rows].double().cpu().numpy()) <= TOL
+    ref = U.radial_backward(plan, xs, ys, hs, alpha, b, gs)
+    for r, a in zip(ref[:3], whole[:3]):
+        assert normalized_error(r, a[rows].double().cpu().numpy()) <= TOL
+
+
 COMPOSED = [
     (24, 2, "canonical", "canonical", 64, {}),      # C % 16 != 0
     (16, 2, "canonical", "canonical", 6, {}),       # H % 4 != 0
