@@ -657,7 +657,8 @@ __device__ __forceinline__ void wgt_step(const float* buf, int edge, int j,
       constexpr int slot = decltype(sc)::value;
       constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
       if constexpr ((ps.mask >> slot) & 1) {
-        const float t = yv[Y.base + ib] * (xv[X.base + ia] * gv[O.base + c]);
+        // x y first: the paths of one (first, second) entry pair share it.
+        const float t = (xv[X.base + ia] * yv[Y.base + ib]) * gv[O.base + c];
         if constexpr ((ps.neg >> slot) & 1)
           gw -= t;
         else
@@ -672,6 +673,91 @@ __device__ __forceinline__ void wgt_step(const float* buf, int edge, int j,
   });
 }
 
+// Direct-to-LDS staging of the affine-adjoint tiles.  buffer_load ... lds
+// writes the 64 floats of one wave instruction to consecutive LDS words from
+// a wave-uniform address (lane l at +4l bytes), so a tile moves from memory
+// to LDS without passing through registers: the tile size costs no registers
+// and there is no separate commit.  The x and g parts of an edge are 16 NC
+// floats at edge * kXS (kChunks 64-float chunks, the last one masked to its
+// kLast valid lanes); y is the tile's contiguous rows (masked past the tile);
+// hidden is one 64-float chunk per edge (zero past a.H).  The chunks are
+// dealt to the waves round-robin.  Completion is counted by vmcnt: the tile
+// is complete once every wave has waited for vmcnt(0) and passed a barrier.
+template <class Plan>
+struct WDma {
+  static constexpr int kXE = 16 * Plan::kComps1;         // x (or g) floats per edge
+  static constexpr int kChunks = (kXE + 63) / 64;         // 64-float chunks per edge
+  static constexpr int kLast = kXE - 64 * (kChunks - 1);  // valid lanes of the last chunk
+};
+
+// Byte offset of this lane's element of every chunk inside an edge's row (the
+// same for every edge and tile of a block; kIdle for the masked lanes).
+template <class Plan>
+__device__ __forceinline__ void wgt_dma_cols(uint32_t (&col)[WDma<Plan>::kChunks], const Args& a,
+                                             int u0, int lane) {
+  static_for<WDma<Plan>::kChunks>([&](auto kc) __attribute__((always_inline)) {
+    constexpr int k = decltype(kc)::value;
+    const int idx = 64 * k + lane;
+    col[k] = idx < WDma<Plan>::kXE ? (uint32_t)tile_x_offset<Plan>(idx, a.C, u0) * 4u : kIdle;
+  });
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One wave instruction: lane l's float at voff goes to dst[l] (dst uniform).
+__device__ __forceinline__ void dma1(__amdgpu_buffer_rsrc_t r, float* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 4, (int)voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Issues this wave's share of tile [t0, t0 + kWeightEdges) into buf.
+template <class Plan, int KH, int NT>
+__device__ __forceinline__ void wgt_dma(float* buf, const Args& a, const float* gout, int64_t t0,
+                                        int64_t t_end, const uint32_t (&col)[WDma<Plan>::kChunks],
+                                        int64_t rows_of_tile, int wave, int lane) {
+  using T = WTile<Plan, KH, NT>;
+  using D = WDma<Plan>;
+  constexpr int W = NT / 64;
+  constexpr int E = Plan::kWeightEdges;
+  static_assert(Geom<KH>::kHid == 64, "one hidden chunk per edge");
+  const int64_t rows = t_end - t0 < E ? t_end - t0 : E;
+  const auto rx = x_rsrc(a, t0, rows);
+  const auto rg = rows_rsrc(gout, t0, a.W1, rows);
+  const auto ry = rows_rsrc(a.y, t0, a.W2, rows);
+  const auto rh = rows_rsrc(a.hidden, t0, a.H, rows);
+  // x and g: (part, edge) pairs; rows past the tile read as zeros.
+  static_for<(2 * E + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
+    const int pr = wave + W * decltype(ic)::value;
+    if (pr < 2 * E) {
+      const bool is_g = pr >= E;
+      const int edge = is_g ? pr - E : pr;
+      uint32_t row = (uint32_t)(edge * a.W1) * 4u;
+      if (!is_g && a.xindex) row = edge < rows ? tile_row_off(a, rows_of_tile, edge) : kIdle;
+      const auto r = is_g ? rg : rx;
+      float* dst = buf + (is_g ? T::kX : 0) + edge * T::kXS;
+      static_for<D::kChunks>([&](auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        const uint32_t off = row == kIdle ? kIdle : row + col[k];
+        if (k + 1 < D::kChunks || lane < D::kLast) dma1(r, dst + 64 * k, off);
+      });
+    }
+  });
+  // y: the tile's rows are contiguous.
+  constexpr int kYC = (T::kY + 63) / 64;
+  float* sy = buf + 2 * T::kX;
+  static_for<(kYC + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
+    const int c = wave + W * decltype(ic)::value;
+    if (c < kYC && 64 * c + lane < T::kY) dma1(ry, sy + 64 * c, (uint32_t)(64 * c + lane) * 4u);
+  });
+  float* sh = sy + T::kY;
+  static_for<(E + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
+    const int edge = wave + W * decltype(ic)::value;
+    if (edge < E)
+      dma1(rh, sh + edge * T::kHS, lane < a.H ? (uint32_t)(edge * a.H + lane) * 4u : kIdle);
+  });
+}
+
 template <class Plan, int KH, int G0>
 __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const float* gout,
                                          int64_t edges_per_slice, float* part_alpha,
@@ -681,10 +767,7 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
   using T = WTile<Plan, KH, NT>;
   constexpr int P = Plan::kPaths;
   constexpr int kWeightEdges = Plan::kWeightEdges;
-  // The first kCoefPad floats of the block's LDS are not used by this kernel
-  // (its couplings are compiled signs and one magnitude per path).
-  constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
-  float* s_tile = s_mem + kCoefPad;
+  float* s_tile = s_mem;  // two tiles (the couplings are compiled signs and magnitudes)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -704,20 +787,20 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
     });
   });
 
-  WCols<Plan, KH, NT> cols;
-  weight_cols<Plan, KH, NT>(cols, a, u0);
-  WPrefetch<Plan, KH, NT> pf;
-  if (tiles > 0) {
-    weight_fetch<Plan, KH, NT>(pf, a, gout, begin, end, cols, tile_rows(a, begin, end));
-    weight_commit<Plan, KH, NT>(pf, s_tile);
-  }
+  uint32_t col[WDma<Plan>::kChunks];
+  wgt_dma_cols<Plan>(col, a, u0, lane);
+  if (tiles > 0)
+    wgt_dma<Plan, KH, NT>(s_tile, a, gout, begin, end, col, tile_rows(a, begin, end), wave, lane);
   int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
+  wait_dma();
   __syncthreads();
   for (int t = 0; t < tiles; ++t) {
-    const bool more = t + 1 < tiles;
-    if (more) {
+    // The next tile streams into the other buffer (read by every wave before
+    // the last barrier) while this one is consumed.
+    if (t + 1 < tiles) {
       const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
-      weight_fetch<Plan, KH, NT>(pf, a, gout, t1, end, cols, next_rows);
+      wgt_dma<Plan, KH, NT>(s_tile + ((t + 1) & 1) * T::kFloats, a, gout, t1, end, col,
+                            next_rows, wave, lane);
       next_rows = tile_rows(a, t1 + kWeightEdges, end);
     }
     const float* buf = s_tile + (t & 1) * T::kFloats;
@@ -728,14 +811,16 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
       constexpr int np = P - q0 < Plan::kWgtPaths ? P - q0 : Plan::kWgtPaths;
       if constexpr (np > 0) {
         if (wave == w) {
-#pragma unroll
+          // Not unrolled: unrolled, the steps' operand loads are hoisted and
+          // the accumulators spill.
+#pragma unroll 1
           for (int s = 0; s < kWeightEdges / 4; ++s) {
             wgt_step<Plan, KH, q0, np>(buf, 4 * s + g, j, ga, gb);
           }
         }
       }
     });
-    if (more) weight_commit<Plan, KH, NT>(pf, s_tile + ((t + 1) & 1) * T::kFloats);
+    wait_dma();
     __syncthreads();
   }
 
@@ -904,8 +989,7 @@ template <class Plan, int KH>
 __global__ __launch_bounds__(64 * kSWgtWaves, 1) void radial_weight_streamed_kernel(
     Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
   using T = WTile<Plan, KH, 64 * kSWgtWaves>;
-  constexpr int kCoefPad = (Plan::kPaths * 8 + 3) / 4 * 4;
-  __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
+  __shared__ __attribute__((aligned(16))) float s_mem[2 * T::kFloats];
   static_for<wgt_groups<Plan>()>([&](auto gc) __attribute__((always_inline)) {
     constexpr int grp = decltype(gc)::value;
     if (blockIdx.z == grp)
