@@ -494,7 +494,19 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
           if constexpr (slot + 1 < kCount)
             wn = weight_tile<KH>(s_mem, bias_off, arow_off, slot + 1, hid);
         }
-        float gw[4] = {0.f, 0.f, 0.f, 0.f};
+        // Per channel row r: G = g w per output component (shared by the
+        // path's slots), T = sum of cy x per output component (gw = g . T),
+        // and the dy contribution of a slot summed over the 4 rows before its
+        // one coupling multiply.
+        float G[2][4], T[2][4];
+        static_for<O.dim>([&](auto occ) __attribute__((always_inline)) {
+          constexpr int oc = decltype(occ)::value;
+          static_for<4>([&](auto rc) __attribute__((always_inline)) {
+            constexpr int r = decltype(rc)::value;
+            G[oc][r] = gv[4 * O.base + r * O.dim + oc] * w[r];
+            T[oc][r] = 0.f;
+          });
+        });
         const auto cfs = load_coefs<ps.mask>(cf, p);
         static_for<8>([&](auto sc2) __attribute__((always_inline)) {
           constexpr int sl = decltype(sc2)::value;
@@ -502,15 +514,22 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
           if constexpr ((ps.mask >> sl) & 1) {
             const float cfv = coef_at<sl>(cfs);
             const float cy = cfv * yv[Y.base + ib];
+            float dsum = 0.f;
             static_for<4>([&](auto rc) __attribute__((always_inline)) {
               constexpr int r = decltype(rc)::value;
               const float xr = xc[r * X.dim + ia];
-              const float gr = gv[4 * O.base + r * O.dim + oc];
-              gw[r] += cy * (xr * gr);
-              dyv[Y.base + ib] += cfv * (xr * gr) * w[r];
-              dxc[r * X.dim + ia] += cy * (gr * w[r]);
+              T[oc][r] += cy * xr;
+              dxc[r * X.dim + ia] += cy * G[oc][r];
+              dsum += xr * G[oc][r];
             });
+            dyv[Y.base + ib] += cfv * dsum;
           }
+        });
+        float gw[4];
+        static_for<4>([&](auto rc) __attribute__((always_inline)) {
+          constexpr int r = decltype(rc)::value;
+          gw[r] = gv[4 * O.base + r * O.dim] * T[0][r];
+          if constexpr (O.dim == 2) gw[r] += gv[4 * O.base + r * O.dim + 1] * T[1][r];
         });
         // Pinned per path (see the forward): unpinned, the dy and dx chains
         // are sunk towards their stores with all their products live.
