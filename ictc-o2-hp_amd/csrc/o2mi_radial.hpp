@@ -314,11 +314,14 @@ __device__ __forceinline__ f4 weight_tile(const float* s_mem, int bias_off, int 
 
 // Staged tile of the affine-adjoint kernel: Plan::kWeightEdges edges of x and g
 // (this block's 16 channels), y and hidden.  Row strides are odd / 16 mod 32
-// so the per-step LDS reads of 4 edges x 16 channels do not collide in banks.
-template <class Plan, int KH, int NT = kThreads>
+// so the per-step LDS reads of 4 edges x 16 channels do not collide in banks
+// (kXPad 1).  An even x row stride (kXPad 2) keeps the two components of an
+// entry 8-byte aligned: they are then read as one 64-bit word at a 16-bit
+// offset, with no address arithmetic.
+template <class Plan, int KH, int NT = kThreads, int kXPad = 1>
 struct WTile {
   static constexpr int kWeightEdges = Plan::kWeightEdges;
-  static constexpr int kXS = 16 * Plan::kComps1 + 1;
+  static constexpr int kXS = 16 * Plan::kComps1 + kXPad;
   static constexpr int kYS = Plan::kComps2;
   static constexpr int kHS = Geom<KH>::kHid + 16;
   static constexpr int kX = kWeightEdges * kXS;

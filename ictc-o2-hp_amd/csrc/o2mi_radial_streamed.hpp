@@ -605,6 +605,10 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
 // wave per SIMD, half the LDS reads per MFMA).
 constexpr int kSWgtWaves = 8;
 
+// The tile of this kernel: even x row stride (64-bit operand reads).
+template <class Plan, int KH>
+using SWTile = WTile<Plan, KH, 64 * kSWgtWaves, 2>;
+
 template <class Plan>
 constexpr int wgt_group_paths() {
   return kSWgtWaves * Plan::kWgtPaths;  // paths per block (grid z)
@@ -631,7 +635,7 @@ __device__ __forceinline__ void wgt_step(const float* buf, int edge, int j,
                                          f4 (&ga)[Plan::kWgtPaths][Geom<KH>::kTiles],
                                          float (&gb)[Plan::kWgtPaths]) {
   using G = Geom<KH>;
-  using T = WTile<Plan, KH, 64 * kSWgtWaves>;
+  using T = SWTile<Plan, KH>;
   const float* sx = buf;
   const float* sg = buf + T::kX;
   const float* sy = buf + 2 * T::kX;
@@ -735,7 +739,7 @@ template <class Plan, int KH, int NT>
 __device__ __forceinline__ void wgt_dma(float* buf, const Args& a, const float* gout, int64_t t0,
                                         int64_t t_end, const uint32_t (&col)[WDma<Plan>::kChunks],
                                         int64_t rows_of_tile, int wave, int lane) {
-  using T = WTile<Plan, KH, NT>;
+  using T = SWTile<Plan, KH>;
   using D = WDma<Plan>;
   constexpr int W = NT / 64;
   constexpr int E = Plan::kWeightEdges;
@@ -783,7 +787,7 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
                                          float* part_bias) {
   constexpr int NT = 64 * kSWgtWaves;
   using G = Geom<KH>;
-  using T = WTile<Plan, KH, NT>;
+  using T = SWTile<Plan, KH>;
   constexpr int P = Plan::kPaths;
   constexpr int kWeightEdges = Plan::kWeightEdges;
   float* s_tile = s_mem;  // two tiles (the couplings are compiled signs and magnitudes)
@@ -1007,7 +1011,7 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
 template <class Plan, int KH>
 __global__ __launch_bounds__(64 * kSWgtWaves, 1) void radial_weight_streamed_kernel(
     Args a, const float* gout, int64_t edges_per_slice, float* part_alpha, float* part_bias) {
-  using T = WTile<Plan, KH, 64 * kSWgtWaves>;
+  using T = SWTile<Plan, KH>;
   __shared__ __attribute__((aligned(16))) float s_mem[2 * T::kFloats];
   static_for<wgt_groups<Plan>()>([&](auto gc) __attribute__((always_inline)) {
     constexpr int grp = decltype(gc)::value;
