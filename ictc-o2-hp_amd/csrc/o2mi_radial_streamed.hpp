@@ -734,50 +734,67 @@ __device__ __forceinline__ void dma1(__amdgpu_buffer_rsrc_t r, float* dst, uint3
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Issues this wave's share of tile [t0, t0 + kWeightEdges) into buf.
+// Descriptor of one edge row of `width` floats (empty when !valid: the row
+// reads as zeros).  Built from uniform values, it lives in scalar registers,
+// so the loads of a row need no per-lane address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* row, int width, bool valid) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), 0, valid ? width * 4 : 0,
+                                           kRsrcFlags);
+}
+
+// Issues this wave's share of tile [t0, t0 + kWeightEdges) into buf.  lane4
+// is the lane's byte offset (4 * lane).
 template <class Plan, int KH, int NT>
 __device__ __forceinline__ void wgt_dma(float* buf, const Args& a, const float* gout, int64_t t0,
                                         int64_t t_end, const uint32_t (&col)[WDma<Plan>::kChunks],
-                                        int64_t rows_of_tile, int wave, int lane) {
+                                        int64_t rows_of_tile, int wave, int lane, uint32_t lane4) {
   using T = SWTile<Plan, KH>;
   using D = WDma<Plan>;
   constexpr int W = NT / 64;
   constexpr int E = Plan::kWeightEdges;
   static_assert(Geom<KH>::kHid == 64, "one hidden chunk per edge");
   const int64_t rows = t_end - t0 < E ? t_end - t0 : E;
-  const auto rx = x_rsrc(a, t0, rows);
-  const auto rg = rows_rsrc(gout, t0, a.W1, rows);
-  const auto ry = rows_rsrc(a.y, t0, a.W2, rows);
-  const auto rh = rows_rsrc(a.hidden, t0, a.H, rows);
-  // x and g: (part, edge) pairs; rows past the tile read as zeros.
+  // x and g: (part, edge) pairs, one row descriptor each; rows past the tile
+  // (and table rows outside the table) read as zeros.
   static_for<(2 * E + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
     const int pr = wave + W * decltype(ic)::value;
     if (pr < 2 * E) {
       const bool is_g = pr >= E;
       const int edge = is_g ? pr - E : pr;
-      uint32_t row = (uint32_t)(edge * a.W1) * 4u;
-      if (!is_g && a.xindex) row = edge < rows ? tile_row_off(a, rows_of_tile, edge) : kIdle;
-      const auto r = is_g ? rg : rx;
+      __amdgpu_buffer_rsrc_t r;
+      if (is_g) {
+        r = row_rsrc(gout + (t0 + edge) * a.W1, a.W1, edge < rows);
+      } else if (a.xindex) {
+        // Lane L of rows_of_tile holds the table row of edge L % 32.
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)rows_of_tile, edge);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)((uint64_t)rows_of_tile >> 32), edge);
+        const int64_t id = (int64_t)(((uint64_t)hi << 32) | lo);
+        const bool ok = edge < rows && id >= 0 && id < a.x_rows;
+        r = row_rsrc(a.x + (ok ? id : 0) * a.W1, a.W1, ok);
+      } else {
+        r = row_rsrc(a.x + (t0 + edge) * a.W1, a.W1, edge < rows);
+      }
       float* dst = buf + (is_g ? T::kX : 0) + edge * T::kXS;
       static_for<D::kChunks>([&](auto kc) __attribute__((always_inline)) {
         constexpr int k = decltype(kc)::value;
-        const uint32_t off = row == kIdle ? kIdle : row + col[k];
-        if (k + 1 < D::kChunks || lane < D::kLast) dma1(r, dst + 64 * k, off);
+        if (k + 1 < D::kChunks || lane < D::kLast) dma1(r, dst + 64 * k, col[k]);
       });
     }
   });
   // y: the tile's rows are contiguous.
   constexpr int kYC = (T::kY + 63) / 64;
   float* sy = buf + 2 * T::kX;
+  const auto ry = rows_rsrc(a.y, t0, a.W2, rows);
   static_for<(kYC + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
     const int c = wave + W * decltype(ic)::value;
-    if (c < kYC && 64 * c + lane < T::kY) dma1(ry, sy + 64 * c, (uint32_t)(64 * c + lane) * 4u);
+    if (c < kYC && 64 * c + lane < T::kY) dma1(ry, sy + 64 * c, (uint32_t)(256 * c) + lane4);
   });
+  // hidden: one row of a.H floats per edge (zeros past a.H).
   float* sh = sy + T::kY;
   static_for<(E + W - 1) / W>([&](auto ic) __attribute__((always_inline)) {
     const int edge = wave + W * decltype(ic)::value;
     if (edge < E)
-      dma1(rh, sh + edge * T::kHS, lane < a.H ? (uint32_t)(edge * a.H + lane) * 4u : kIdle);
+      dma1(row_rsrc(a.hidden + (t0 + edge) * a.H, a.H, edge < rows), sh + edge * T::kHS, lane4);
   });
 }
 
@@ -812,8 +829,10 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
 
   uint32_t col[WDma<Plan>::kChunks];
   wgt_dma_cols<Plan>(col, a, u0, lane);
+  const uint32_t lane4 = 4u * (uint32_t)lane;
   if (tiles > 0)
-    wgt_dma<Plan, KH, NT>(s_tile, a, gout, begin, end, col, tile_rows(a, begin, end), wave, lane);
+    wgt_dma<Plan, KH, NT>(s_tile, a, gout, begin, end, col, tile_rows(a, begin, end), wave, lane,
+                          lane4);
   int64_t next_rows = tile_rows(a, begin + kWeightEdges, end);
   wait_dma();
   __syncthreads();
@@ -823,7 +842,7 @@ __device__ __forceinline__ void wgt_body(float* s_mem, const Args& a, const floa
     if (t + 1 < tiles) {
       const int64_t t1 = begin + (int64_t)(t + 1) * kWeightEdges;
       wgt_dma<Plan, KH, NT>(s_tile + ((t + 1) & 1) * T::kFloats, a, gout, t1, end, col,
-                            next_rows, wave, lane);
+                            next_rows, wave, lane, lane4);
       next_rows = tile_rows(a, t1 + kWeightEdges, end);
     }
     const float* buf = s_tile + (t & 1) * T::kFloats;
