@@ -675,18 +675,24 @@ __device__ __forceinline__ void wgt_step(const float* buf, int edge, int j,
     // The path's weight adjoint divided by its coupling magnitude: the
     // couplings' signs are compiled, the magnitude is applied once to the
     // finished sums (wgt_body), so no coupling is read per step.
+    // Per output component T = sum of the signed x y products (shared by the
+    // paths of one (first, second) entry pair), gw = sum of g T.
     float gw = 0.f;
-    static_for<8>([&](auto sc) __attribute__((always_inline)) {
-      constexpr int slot = decltype(sc)::value;
-      constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-      if constexpr ((ps.mask >> slot) & 1) {
-        // x y first: the paths of one (first, second) entry pair share it.
-        const float t = (xv[X.base + ia] * yv[Y.base + ib]) * gv[O.base + c];
-        if constexpr ((ps.neg >> slot) & 1)
-          gw -= t;
-        else
-          gw += t;
-      }
+    static_for<O.dim>([&](auto occ) __attribute__((always_inline)) {
+      constexpr int c = decltype(occ)::value;
+      float t = 0.f;
+      static_for<4>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int slot = c * 4 + decltype(sc)::value;
+        constexpr int ia = (slot >> 1) & 1, ib = slot & 1;
+        if constexpr ((ps.mask >> slot) & 1) {
+          const float xy = xv[X.base + ia] * yv[Y.base + ib];
+          if constexpr ((ps.neg >> slot) & 1)
+            t -= xy;
+          else
+            t += xy;
+        }
+      });
+      gw += gv[O.base + c] * t;
     });
     gb[q] += gw;
     static_for<G::kTiles>([&](auto tc) __attribute__((always_inline)) {

@@ -115,27 +115,42 @@ template <class Plan, int KH>
 __device__ __forceinline__ void gw_form(const GwOperands<Plan>& op, float* gw, float* hb, int el,
                                         int cp) {
   using L = GwLayout<Plan, KH>;
+  float z[2][2][2];  // [ia][ib][channel of the pair]
   static_for<Plan::kPaths>([&](auto qc) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value;
     constexpr RPath ps = Plan::paths[Plan::wgt[q]];
     constexpr REntry X = Plan::e1[ps.i];
     constexpr REntry Y = Plan::e2[ps.j];
     constexpr REntry O = Plan::e1[ps.k];
+    // The x y products of a (first, second) entry pair, shared by its paths
+    // (consecutive in Plan::wgt); per output component T = sum of the signed
+    // products, gw = sum over components of g T.
+    constexpr bool first = q == 0 || Plan::paths[Plan::wgt[q == 0 ? 0 : q - 1]].i != ps.i ||
+                           Plan::paths[Plan::wgt[q == 0 ? 0 : q - 1]].j != ps.j;
+    if constexpr (first)
+      static_for<X.dim * Y.dim * 2>([&](auto zc) __attribute__((always_inline)) {
+        constexpr int ia = decltype(zc)::value / (2 * Y.dim);
+        constexpr int ib = decltype(zc)::value / 2 % Y.dim, k = decltype(zc)::value % 2;
+        z[ia][ib][k] = op.x[X.base + ia][k] * op.y[Y.base + ib];
+      });
     f2v v = {0.f, 0.f};
-    static_for<8>([&](auto sc) __attribute__((always_inline)) {
-      constexpr int slot = decltype(sc)::value;
-      constexpr int oc = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-      if constexpr ((ps.mask >> slot) & 1) {
-        const float yv = op.y[Y.base + ib];
-        static_for<2>([&](auto kc) __attribute__((always_inline)) {
-          constexpr int k = decltype(kc)::value;
-          const float t = yv * (op.x[X.base + ia][k] * op.g[O.base + oc][k]);
-          if constexpr ((ps.neg >> slot) & 1)
-            v[k] -= t;
-          else
-            v[k] += t;
+    static_for<2>([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      static_for<O.dim>([&](auto occ) __attribute__((always_inline)) {
+        constexpr int oc = decltype(occ)::value;
+        float t = 0.f;
+        static_for<4>([&](auto sc) __attribute__((always_inline)) {
+          constexpr int slot = oc * 4 + decltype(sc)::value;
+          constexpr int ia = (slot >> 1) & 1, ib = slot & 1;
+          if constexpr ((ps.mask >> slot) & 1) {
+            if constexpr ((ps.neg >> slot) & 1)
+              t -= z[ia][ib][k];
+            else
+              t += z[ia][ib][k];
+          }
         });
-      }
+        v[k] += op.g[O.base + oc][k] * t;
+      });
     });
     *reinterpret_cast<f2v*>(gw + (q * kGwEdges + el) * 16 + 2 * cp) = v;
   });
