@@ -919,8 +919,9 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
   constexpr int kE = TP::kWeightEdges;
   constexpr int NPW = (P + kWaves - 1) / kWaves;
   constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
+  // The first kCoefPad floats are unused (the couplings' signs are compiled);
+  // they keep the tile size that dw_edges() chose for this layout.
   __shared__ __attribute__((aligned(16))) float s_mem[kCoefPad + 2 * T::kFloats];
-  float* s_coef = s_mem;
   float* s_tile = s_mem + kCoefPad;
 
   const int lane = threadIdx.x & 63;
@@ -931,7 +932,6 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
   const int64_t end = begin + edges_per_slice < a.n ? begin + edges_per_slice : a.n;
   const int tiles = end > begin ? (int)((end - begin + kE - 1) / kE) : 0;
 
-  for (int idx = threadIdx.x; idx < P * 8; idx += kThreads) s_coef[idx] = a.coef[idx];
   float acc[NPW];
   static_for<NPW>([&](auto qc) __attribute__((always_inline)) { acc[decltype(qc)::value] = 0.f; });
 
@@ -961,12 +961,9 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
       constexpr int np = P - q0 < NPW ? P - q0 : NPW;
       if constexpr (np > 0) {
         if (wave == w) {
-#pragma unroll 2
+#pragma unroll 1
           for (int s = 0; s < kE / 4; ++s) {
             const int edge = 4 * s + g;
-            int coef_off = 0;
-            asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
-            const float* cf = s_coef + coef_off;
             float xv[Plan::kComps1], gv[Plan::kComps1], yv[Plan::kComps2];
             static_for<Plan::kEntries1>([&](auto ec) __attribute__((always_inline)) {
               constexpr int e = decltype(ec)::value;
@@ -989,6 +986,11 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
                   yv[E.base + d] = sy[edge * T::kYS + E.base + d];
                 });
             });
+            // Per path: the signed x y products of its (first, second) entry
+            // pair (shared by the pair's consecutive paths), summed per output
+            // component into T, then acc += g . T.  The couplings' magnitudes
+            // scale the finished sums.
+            float z[2][2];
             static_for<np>([&](auto qc) __attribute__((always_inline)) {
               constexpr int q = decltype(qc)::value;
               constexpr int p = Plan::wgt[q0 + q];
@@ -996,13 +998,28 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
               constexpr REntry X = Plan::e1[ps.i];
               constexpr REntry Y = Plan::e2[ps.j];
               constexpr REntry O = Plan::e1[ps.k];
-              const auto cfs = load_coefs<ps.mask>(cf, p);
-              static_for<8>([&](auto sc) __attribute__((always_inline)) {
-                constexpr int slot = decltype(sc)::value;
-                constexpr int c = slot >> 2, ia = (slot >> 1) & 1, ib = slot & 1;
-                if constexpr ((ps.mask >> slot) & 1)
-                  acc[q] += coef_at<slot>(cfs) * yv[Y.base + ib] *
-                            (xv[X.base + ia] * gv[O.base + c]);
+              constexpr bool first = q == 0 ||
+                                     Plan::paths[Plan::wgt[q0 + (q == 0 ? 0 : q - 1)]].i != ps.i ||
+                                     Plan::paths[Plan::wgt[q0 + (q == 0 ? 0 : q - 1)]].j != ps.j;
+              if constexpr (first)
+                static_for<X.dim * Y.dim>([&](auto zc) __attribute__((always_inline)) {
+                  constexpr int ia = decltype(zc)::value / Y.dim, ib = decltype(zc)::value % Y.dim;
+                  z[ia][ib] = xv[X.base + ia] * yv[Y.base + ib];
+                });
+              static_for<O.dim>([&](auto occ) __attribute__((always_inline)) {
+                constexpr int c = decltype(occ)::value;
+                float t = 0.f;
+                static_for<4>([&](auto sc) __attribute__((always_inline)) {
+                  constexpr int slot = c * 4 + decltype(sc)::value;
+                  constexpr int ia = (slot >> 1) & 1, ib = slot & 1;
+                  if constexpr ((ps.mask >> slot) & 1) {
+                    if constexpr ((ps.neg >> slot) & 1)
+                      t -= z[ia][ib];
+                    else
+                      t += z[ia][ib];
+                  }
+                });
+                acc[q] += gv[O.base + c] * t;
               });
             });
           }
@@ -1022,10 +1039,12 @@ __global__ __launch_bounds__(kThreads, 1) void uvu_shared_dw_kernel(Args a, cons
       if (wave == w) {
         static_for<np>([&](auto qc) __attribute__((always_inline)) {
           constexpr int q = decltype(qc)::value;
+          constexpr int p = Plan::wgt[q0 + q];
           float v = acc[q];
           v += __shfl_xor(v, 16);
           v += __shfl_xor(v, 32);
-          if (g == 0) dst[(int64_t)Plan::wgt[q0 + q] * a.C + u0 + j] = v;
+          const float mag = fabsf(a.coef[p * 8 + first_slot(Plan::paths[p].mask)]);
+          if (g == 0) dst[(int64_t)p * a.C + u0 + j] = v * mag;
         });
       }
     }
