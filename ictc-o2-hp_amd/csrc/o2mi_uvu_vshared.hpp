@@ -469,8 +469,8 @@ __device__ __forceinline__ void vtile_commit(const VPrefetch<Plan, kE, NT>& pf, 
 // (g, j) forms gz for edge 4s + g and channel u0 + j (the A operand) and
 // supplies copy j of the edge's components (the B operand).
 template <class Plan, int kE, int NT, int Q0, int NPW>
-__device__ __forceinline__ void vdw_step(const float* buf, const float* cf, int V, int W2,
-                                         int edge, int j, f4 (&acc)[vdw_paths<Plan>()]) {
+__device__ __forceinline__ void vdw_step(const float* buf, int V, int W2, int edge, int j,
+                                         f4 (&acc)[vdw_paths<Plan>()]) {
   using T = VTile<Plan, kE, NT>;
   const float* sx = buf;
   const float* sg = buf + T::kX;
@@ -506,15 +506,20 @@ __device__ __forceinline__ void vdw_step(const float* buf, const float* cf, int 
     constexpr REntry X = Plan::e1[ps.i];
     constexpr REntry Y = Plan::e2[ps.j];
     constexpr REntry O = Plan::e1[ps.k];
-    const auto cfs = load_coefs<ps.mask>(cf, p);
+    // The couplings' signs are compiled (one FMA per slot); their magnitude
+    // scales the finished sums.
     static_for<Y.dim>([&](auto bc) __attribute__((always_inline)) {
       constexpr int ib = decltype(bc)::value;
       float gz = 0.f;
       static_for<8>([&](auto sc) __attribute__((always_inline)) {
         constexpr int sl = decltype(sc)::value;
         constexpr int oc = sl >> 2, ia = (sl >> 1) & 1;
-        if constexpr (((ps.mask >> sl) & 1) && (sl & 1) == ib)
-          gz += coef_at<sl>(cfs) * (xv[X.base + ia] * gv[O.base + oc]);
+        if constexpr (((ps.mask >> sl) & 1) && (sl & 1) == ib) {
+          if constexpr ((ps.neg >> sl) & 1)
+            gz -= xv[X.base + ia] * gv[O.base + oc];
+          else
+            gz += xv[X.base + ia] * gv[O.base + oc];
+        }
       });
       acc[q] = mfma(gz, yv[Y.base + ib], acc[q]);
     });
@@ -530,8 +535,9 @@ __device__ __forceinline__ void vdw_body(float* s_mem, const Args& a, const floa
   using T = VTile<Plan, kE, NT>;
   constexpr int P = Plan::kPaths;
   constexpr int XE = 16 * Plan::kComps1;
+  // The first kCoefPad floats are unused (the couplings' signs are compiled);
+  // they keep the tile size that vdw_edges() chose for this layout.
   constexpr int kCoefPad = (P * 8 + 3) / 4 * 4;
-  float* s_coef = s_mem;
   float* s_tile = s_mem + kCoefPad;
 
   const int lane = threadIdx.x & 63;
@@ -543,7 +549,6 @@ __device__ __forceinline__ void vdw_body(float* s_mem, const Args& a, const floa
   const int tiles = end > begin ? (int)((end - begin + kE - 1) / kE) : 0;
   const int nv = a.V, w2 = a.W2;
 
-  for (int idx = threadIdx.x; idx < P * 8; idx += NT) s_coef[idx] = a.coef[idx];
   f4 acc[NPW];
   static_for<NPW>([&](auto qc) __attribute__((always_inline)) { acc[decltype(qc)::value] = f4{0.f, 0.f, 0.f, 0.f}; });
 
@@ -574,11 +579,8 @@ __device__ __forceinline__ void vdw_body(float* s_mem, const Args& a, const floa
       if constexpr (np > 0) {
         if (wave == w) {
 #pragma unroll
-          for (int s = 0; s < kE / 4; ++s) {
-            int coef_off = 0;
-            asm volatile("" : "+v"(coef_off));  // re-read couplings per step, do not hoist
-            vdw_step<Plan, kE, NT, q0, np>(buf, s_coef + coef_off, nv, w2, 4 * s + g, j, acc);
-          }
+          for (int s = 0; s < kE / 4; ++s)
+            vdw_step<Plan, kE, NT, q0, np>(buf, nv, w2, 4 * s + g, j, acc);
         }
       }
     });
@@ -596,10 +598,12 @@ __device__ __forceinline__ void vdw_body(float* s_mem, const Args& a, const floa
       if (wave == w && j < a.V) {
         static_for<np>([&](auto qc) __attribute__((always_inline)) {
           constexpr int q = decltype(qc)::value;
-          const int64_t row = (int64_t)Plan::wgt[q0 + q] * a.C + u0 + 4 * g;
+          constexpr int p = Plan::wgt[q0 + q];
+          const int64_t row = (int64_t)p * a.C + u0 + 4 * g;
+          const float mag = fabsf(a.coef[p * 8 + first_slot(Plan::paths[p].mask)]);
           static_for<4>([&](auto rc) __attribute__((always_inline)) {
             constexpr int r = decltype(rc)::value;
-            dst[(row + r) * a.V + j] = acc[q][r];
+            dst[(row + r) * a.V + j] = acc[q][r] * mag;
           });
         });
       }
