@@ -100,15 +100,17 @@ int stream_splits(const o2mi_radial_plan* p, int64_t n) {
   return (p->C + span - 1) / span;
 }
 
-// The per-row weight kernels' channel span: as stream_span, for their 64-edge
-// blocks and 32-channel tiles.
+// The per-row weight kernels' channel span: as stream_span, for their edge
+// blocks and the 32 row_pairs(C) channels an edge group covers per round.
 int row_span(const o2mi_radial_plan* p, int64_t n) {
-  const int64_t blocks = std::max<int64_t>(1, (n + kRowStreamEdges - 1) / kRowStreamEdges);
+  const int per_block = row_stream_edges(p->C);
+  const int64_t blocks = std::max<int64_t>(1, (n + per_block - 1) / per_block);
   const int64_t cus = device_cus();
-  const int tiles = (p->C + 31) / 32;
+  const int round = 32 * row_pairs(p->C);
+  const int tiles = (p->C + round - 1) / round;
   if (blocks >= cus || tiles == 1) return p->C;
   const int64_t want = std::min<int64_t>(tiles, (cus + blocks - 1) / blocks);
-  return std::min(p->C, 32 * (int)((tiles + want - 1) / want));
+  return std::min(p->C, round * (int)((tiles + want - 1) / want));
 }
 
 int row_splits(const o2mi_radial_plan* p, int64_t n) {

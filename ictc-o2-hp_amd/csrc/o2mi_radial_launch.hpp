@@ -108,11 +108,13 @@ hipError_t launch_shared_backward(const Args& a, const float* gout, float* gx, f
   return hipGetLastError();
 }
 
-// Per-row weights: waves in pairs over 32-channel tiles, 64 edges per block.
-constexpr int kRowStreamEdges = kStreamEdges / 2;
+// Per-row weights: waves in pairs over 32-channel tiles, 16 edges per group
+// of row_pairs(C) pairs (16 edges per block at C >= 128, 64 below C = 64).
+inline int row_stream_edges(int C) { return kStreamEdges / 2 / row_pairs(C); }
 
 inline dim3 row_grid(const Args& a) {
-  return dim3((unsigned)((a.n + kRowStreamEdges - 1) / kRowStreamEdges),
+  const int per_block = row_stream_edges(a.C);
+  return dim3((unsigned)((a.n + per_block - 1) / per_block),
               (unsigned)((a.C + a.tile_span - 1) / a.tile_span));
 }
 

@@ -155,6 +155,14 @@ constexpr int kAffineW = 0, kSharedW = 1, kRowW = 2;
 // kRowAhead; the ring restarts at each tile, one load latency per tile).
 constexpr int kRowAhead = 2;
 
+// kRowW: the block's 4 wave pairs form 4 / row_pairs(C) edge groups of 16
+// edges, and the row_pairs(C) pairs of a group take its 32-channel tiles
+// round-robin.  A group then reads up to 512 contiguous bytes of each
+// (edge, path) weight segment together and a block's weights are whole
+// consecutive rows (2 MB at C128 m4 full), instead of 4 edge groups each
+// revisiting its rows once per 32-channel tile.
+__host__ __device__ constexpr int row_pairs(int C) { return C >= 128 ? 4 : (C >= 64 ? 2 : 1); }
+
 // kRowW: cache policy of the per-row weight-adjoint stores.  Default
 // (write-back) lets L2 merge the two halves of a 128-byte line that the two
 // waves of a pair write at about the same time; non-temporal 16-byte stores
@@ -197,14 +205,18 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, j = lane & 15;
-  // kRowW: waves in pairs, one pair per 16 edges; the two waves of a pair take
-  // the two 16-channel halves of a 32-channel tile, so the two halves of each
-  // 128-byte line of a row's weights are read by one CU at about the same time
-  // (one 16-channel tile per pass read every line twice from HBM).
+  // kRowW: waves in pairs; the two waves of a pair take the two 16-channel
+  // halves of a 32-channel tile, so the two halves of each 128-byte line of a
+  // row's weights are read by one CU at about the same time (one 16-channel
+  // tile per pass read every line twice from HBM).  Pairs sharing an edge
+  // group (row_pairs) take its tiles round-robin, slot `rsub`.
   const int half = kMode == kRowW ? (wave & 1) : 0;
-  const int64_t e0 = kMode == kRowW
-                         ? ((int64_t)blockIdx.x * (NT / 128) + (wave >> 1)) * kEdgesPerWave
-                         : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const int rpg = kMode == kRowW ? row_pairs(a.C) : 1;
+  const int rsub = kMode == kRowW ? (wave >> 1) % rpg : 0;
+  const int64_t e0 =
+      kMode == kRowW
+          ? ((int64_t)blockIdx.x * ((NT / 128) / rpg) + (wave >> 1) / rpg) * kEdgesPerWave
+          : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
@@ -234,14 +246,15 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   constexpr int ND1 = dim1_before<Plan>(Plan::kEntries1);
   float xcarry[4 * (ND1 > 0 ? ND1 : 1)] = {};
   int parity = 0;  // LDS buffer of the current chunk
-  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
+  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 * rpg : 16)) {
     __syncthreads();
     if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
-    if (kMode == kRowW && u0 + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
-    const int u = u0 + 16 * half + 4 * g;
+    const int ut = u0 + 32 * rsub;  // this pair's 32-channel tile (kRowW; u0 otherwise)
+    if (kMode == kRowW && ut + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
+    const int u = ut + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, false>(ring, rw, wrow, a.C);
     // kRowW: the two waves of a pair read both halves of a line already.
@@ -348,14 +361,18 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, j = lane & 15;
-  // kRowW: waves in pairs, one pair per 16 edges; the two waves of a pair take
-  // the two 16-channel halves of a 32-channel tile, so the two halves of each
-  // 128-byte line of a row's weights are read by one CU at about the same time
-  // (one 16-channel tile per pass read every line twice from HBM).
+  // kRowW: waves in pairs; the two waves of a pair take the two 16-channel
+  // halves of a 32-channel tile, so the two halves of each 128-byte line of a
+  // row's weights are read by one CU at about the same time (one 16-channel
+  // tile per pass read every line twice from HBM).  Pairs sharing an edge
+  // group (row_pairs) take its tiles round-robin, slot `rsub`.
   const int half = kMode == kRowW ? (wave & 1) : 0;
-  const int64_t e0 = kMode == kRowW
-                         ? ((int64_t)blockIdx.x * (NT / 128) + (wave >> 1)) * kEdgesPerWave
-                         : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const int rpg = kMode == kRowW ? row_pairs(a.C) : 1;
+  const int rsub = kMode == kRowW ? (wave >> 1) % rpg : 0;
+  const int64_t e0 =
+      kMode == kRowW
+          ? ((int64_t)blockIdx.x * ((NT / 128) / rpg) + (wave >> 1) / rpg) * kEdgesPerWave
+          : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto rg = rows_rsrc(gout, e0, a.W1, rows);
@@ -403,14 +420,15 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   constexpr bool kPair = kMode == kAffineW && ND1 == 1 && 4 * NC + 2 * NY <= 72;
   float gcarry[4 * (ND1 > 0 ? ND1 : 1)] = {}, xcarry[4 * (ND1 > 0 ? ND1 : 1)] = {};
   int parity = 0;
-  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 : 16)) {
+  for (int u0 = u_begin; u0 < u_end; u0 += (kMode == kRowW ? 32 * rpg : 16)) {
     __syncthreads();
     if constexpr (kMode == kSharedW) {
       stage_shared_weights<Plan, NT>(s_mem + L::kBuf0, a, u0);
       __syncthreads();
     }
-    if (kMode == kRowW && u0 + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
-    const int u = u0 + 16 * half + 4 * g;
+    const int ut = u0 + 32 * rsub;  // this pair's 32-channel tile (kRowW; u0 otherwise)
+    if (kMode == kRowW && ut + 16 * half >= u_end) continue;  // wave-uniform; barriers stay paired
+    const int u = ut + 16 * half + 4 * g;
     const uint32_t wrow = (uint32_t)(j * P * a.C + u) * 4u;  // kRowW: path 0 of this lane
     if constexpr (kMode == kRowW) row_prologue<Plan, true>(ring, rw, wrow, a.C);
     const TilePair tp = tile_pair(kPair, u0, u_begin, u_end);
@@ -573,16 +591,19 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
       dyv[c] += __shfl_xor(dyv[c], 32);
     });
     if constexpr (kMode == kRowW) {
-      static_assert((NT / 128) * 16 * NY <= 2 * L::kBufFloats, "dy exchange fits the buffers");
-      // The pair's second wave hands its channel half's sums to the first.
-      float* s_dy = s_mem + L::kBuf0 + (wave >> 1) * 16 * NY;
-      if (half == 1 && g == 0)
-        static_for<NY>([&](auto cc) __attribute__((always_inline)) { s_dy[j * NY + decltype(cc)::value] = dyv[decltype(cc)::value]; });
+      static_assert((NT / 64) * 16 * NY <= 2 * L::kBufFloats, "dy exchange fits the buffers");
+      // Every wave of an edge group but its first hands its channels' sums to
+      // the first, which adds them in wave order (a fixed order).
+      float* s_dy = s_mem + L::kBuf0;
+      const int lead = wave - 2 * rsub - half;  // first wave of this edge group
+      if (wave != lead && g == 0)
+        static_for<NY>([&](auto cc) __attribute__((always_inline)) { s_dy[(wave * 16 + j) * NY + decltype(cc)::value] = dyv[decltype(cc)::value]; });
       __syncthreads();
-      if (half == 0)
-        static_for<NY>([&](auto cc) __attribute__((always_inline)) { dyv[decltype(cc)::value] += s_dy[j * NY + decltype(cc)::value]; });
+      if (wave == lead)
+        for (int k = 1; k < 2 * rpg; ++k)
+          static_for<NY>([&](auto cc) __attribute__((always_inline)) { dyv[decltype(cc)::value] += s_dy[((lead + k) * 16 + j) * NY + decltype(cc)::value]; });
     }
-    if (g == 0 && j < rows && half == 0) {
+    if (g == 0 && j < rows && half == 0 && rsub == 0) {
       float* dst = dy_base + (e0 + j) * a.W2;
       static_for<NY>([&](auto cc) __attribute__((always_inline)) { dst[decltype(cc)::value] = dyv[decltype(cc)::value]; });
     }
