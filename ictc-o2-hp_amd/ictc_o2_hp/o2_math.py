@@ -21,8 +21,9 @@ the reference's names and signatures so code written against the reference's
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 from functools import lru_cache
-from typing import List, Tuple
+from typing import Dict, List, Tuple
 
 import numpy as np
 import torch
@@ -250,6 +251,27 @@ def o2_cg_tensor(key1, key2, key3, *, dtype=None, device=None) -> torch.Tensor:
     if dtype is not None or device is not None:
         out = out.to(dtype=dtype, device=device)
     return out
+
+
+@dataclass(frozen=True)
+class HarmonicProjectors2D:
+    """Frequency projectors of the degree-L Cartesian polynomials, L <= Lmax.
+
+    ``P[(L, m)]`` (m = L, L-2, ..., shape (dim(m), L+1), float64) maps the
+    monomial coefficients of a degree-L polynomial to its coordinates on the
+    frequency-m harmonics lifted by (x^2 + y^2)^((L-m)/2), orthogonally under
+    the Gaussian Gram matrix (``o2_math.py:140-157``)."""
+    Lmax: int
+    P: Dict[Tuple[int, int], torch.Tensor]
+
+
+@lru_cache(maxsize=None)
+def build_harmonic_projectors_2d(Lmax: int) -> HarmonicProjectors2D:
+    """All projectors ``P[(L, m)]`` for 0 <= L <= Lmax (``o2_math.py:144-157``)."""
+    Lmax = int(Lmax)
+    table = {(L, L - 2 * k): torch.from_numpy(_projector(L, L - 2 * k).copy())
+             for L in range(Lmax + 1) for k in range(L // 2 + 1)}
+    return HarmonicProjectors2D(Lmax=Lmax, P=table)
 
 
 def build_cg_tensor_so2(m1: int, m2: int, m3: int) -> torch.Tensor:

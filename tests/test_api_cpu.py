@@ -153,6 +153,66 @@ def test_missing_library_raises(monkeypatch, tmp_path):
         _native.library()
 
 
+def _monomial_values(L, pts):
+    """x^a y^(L-a) at the points, a = 0..L (the monomial order of the projectors)."""
+    return np.stack([pts[:, 0] ** a * pts[:, 1] ** (L - a) for a in range(L + 1)], axis=1)
+
+
+@pytest.mark.parametrize("L", [0, 1, 2, 5, 8])
+def test_harmonic_projectors_split_polynomials_by_frequency(L):
+    """build_harmonic_projectors_2d (o2_math.py:140-157): P[(L, m)] has one
+    row per frequency-m harmonic, reads back the frequency-m part of
+    r^(L-m) * (Re, Im)(x + i y)^m exactly (up to the basis' sign and scale) and
+    nothing of the other frequencies, and rotations of the plane act on each
+    P[(L, m)] a as norm-preserving maps (checked by refitting rotated
+    polynomials from point values)."""
+    from ictc_o2_hp import o2_math
+    proj = o2_math.build_harmonic_projectors_2d(L)
+    ms = [L - 2 * k for k in range(L // 2 + 1)]
+    assert proj.Lmax == L and set(proj.P) == {(l, l - 2 * k) for l in range(L + 1)
+                                             for k in range(l // 2 + 1)}
+    rng = np.random.default_rng(L)
+    pts = rng.standard_normal((4 * (L + 1), 2))
+    mono = _monomial_values(L, pts)
+    r2 = (pts ** 2).sum(axis=1)
+    z = pts[:, 0] + 1j * pts[:, 1]
+    for m in ms:
+        P = proj.P[(L, m)].numpy()
+        assert P.shape == (o2_math.so2_irrep_dim(m), L + 1) and P.dtype == np.float64
+        for m2 in ms:
+            parts = [np.real(z ** m2)] + ([np.imag(z ** m2)] if m2 > 0 else [])
+            for part in parts:
+                values = r2 ** ((L - m2) // 2) * part
+                coeffs = np.linalg.lstsq(mono, values, rcond=None)[0]
+                got = P @ coeffs
+                if m2 != m:
+                    assert np.abs(got).max() < 1e-9 * max(1.0, np.abs(coeffs).max())
+                else:
+                    assert np.abs(got).max() > 1e-6
+    # Rotation by t: p(R^-1 v) has the same frequency-m norm as p.
+    a = rng.standard_normal(L + 1)
+    t = 0.7
+    rot = np.array([[np.cos(t), np.sin(t)], [-np.sin(t), np.cos(t)]])
+    rotated = np.linalg.lstsq(mono, _monomial_values(L, pts @ rot.T) @ a, rcond=None)[0]
+    for m in ms:
+        P = proj.P[(L, m)].numpy()
+        assert abs(np.linalg.norm(P @ rotated) - np.linalg.norm(P @ a)) < 1e-8 * (1 + np.linalg.norm(P @ a))
+
+
+def test_harmonic_projectors_planted_mistake_is_caught():
+    """A projector built with the identity instead of the Gaussian Gram matrix
+    mixes frequencies: its frequency-0 row of degree 4 sees Re (x + i y)^4."""
+    from ictc_o2_hp import o2_math
+    L, m = 4, 0
+    lifted = o2_math._radial_lift(m, 2) @ o2_math._harmonic_basis(m)
+    wrong = np.linalg.solve(lifted.T @ lifted, lifted.T)
+    pts = np.random.default_rng(1).standard_normal((20, 2))
+    z = pts[:, 0] + 1j * pts[:, 1]
+    coeffs = np.linalg.lstsq(_monomial_values(L, pts), np.real(z ** 4), rcond=None)[0]
+    assert np.abs(o2_math.build_harmonic_projectors_2d(L).P[(L, m)].numpy() @ coeffs).max() < 1e-9
+    assert np.abs(wrong @ coeffs).max() > 1e-3
+
+
 def test_o2_math_public_functions():
     from ictc_o2_hp import o2_math
     assert o2_math.o2_valid_output_keys("2", "2") == [("scalar", 1), ("scalar", -1), ("freq", 4)]
