@@ -171,7 +171,9 @@ def test_uvu_shared_v_roles_and_reproducible():
 # them): the streamed radial kernels reading each row's weights from memory.
 ROWS_V1 = [
     (64, 4, {"parity": "canonical"}, 700),                                # configs[4] TP shape
-    (128, 4, {"parity": "full"}, 100),                                    # channels split
+    (128, 4, {"parity": "full"}, 100),                                    # 4 pairs, one edge group
+    (256, 2, {"parity": "full"}, 50),                                     # 128-channel spans over grid y
+    (96, 2, {"parity": "canonical"}, 90),                                 # idle pair; 64 + 32 channel spans
     (32, 6, {"parity": "full", "parity_in2": "canonical"}, 300),
     (48, 3, {"parity": "canonical", "parity_in2": "full", "path_normalization": "path"}, 70),
     (16, 0, {"parity": "full", "normalization": "norm"}, 1),
