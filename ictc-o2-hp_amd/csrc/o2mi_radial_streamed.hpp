@@ -163,6 +163,23 @@ constexpr int kRowAhead = 2;
 // revisiting its rows once per 32-channel tile.
 __host__ __device__ constexpr int row_pairs(int C) { return C >= 128 ? 4 : (C >= 64 ? 2 : 1); }
 
+// kRowW: what wave `wave` of block `block` (`waves` per block) covers: edges
+// [e0, e0 + 16) and, within the block's channel span [u_begin, u_end), the
+// 16 channels at u0 + 32 sub + 16 half of each round u0 = u_begin,
+// u_begin + 32 pairs, ... that start below u_end.
+struct RowWave {
+  int64_t e0;
+  int sub;    // the wave's pair among the edge group's pairs
+  int pairs;  // pairs per edge group: row_pairs(C)
+  int half;   // 16-channel half of the pair's 32-channel tile
+};
+
+__host__ __device__ constexpr RowWave row_wave(int C, int64_t block, int wave, int waves) {
+  const int pairs = row_pairs(C);
+  return RowWave{(block * ((waves / 2) / pairs) + (wave >> 1) / pairs) * kEdgesPerWave,
+                 (wave >> 1) % pairs, pairs, wave & 1};
+}
+
 // kRowW: cache policy of the per-row weight-adjoint stores.  Default
 // (write-back) lets L2 merge the two halves of a 128-byte line that the two
 // waves of a pair write at about the same time; non-temporal 16-byte stores
@@ -210,13 +227,12 @@ __global__ __launch_bounds__(64 * kSFwdWaves, 1) void radial_forward_streamed_ke
   // row's weights are read by one CU at about the same time (one 16-channel
   // tile per pass read every line twice from HBM).  Pairs sharing an edge
   // group (row_pairs) take its tiles round-robin, slot `rsub`.
-  const int half = kMode == kRowW ? (wave & 1) : 0;
-  const int rpg = kMode == kRowW ? row_pairs(a.C) : 1;
-  const int rsub = kMode == kRowW ? (wave >> 1) % rpg : 0;
-  const int64_t e0 =
-      kMode == kRowW
-          ? ((int64_t)blockIdx.x * ((NT / 128) / rpg) + (wave >> 1) / rpg) * kEdgesPerWave
-          : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const RowWave wmap = row_wave(a.C, blockIdx.x, wave, NT / 64);
+  const int half = kMode == kRowW ? wmap.half : 0;
+  const int rpg = kMode == kRowW ? wmap.pairs : 1;
+  const int rsub = kMode == kRowW ? wmap.sub : 0;
+  const int64_t e0 = kMode == kRowW ? wmap.e0
+                                    : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto ry = rows_rsrc(a.y, e0, a.W2, rows);
@@ -366,13 +382,12 @@ __global__ __launch_bounds__(64 * kSBwdWaves, 1) void radial_backward_streamed_k
   // row's weights are read by one CU at about the same time (one 16-channel
   // tile per pass read every line twice from HBM).  Pairs sharing an edge
   // group (row_pairs) take its tiles round-robin, slot `rsub`.
-  const int half = kMode == kRowW ? (wave & 1) : 0;
-  const int rpg = kMode == kRowW ? row_pairs(a.C) : 1;
-  const int rsub = kMode == kRowW ? (wave >> 1) % rpg : 0;
-  const int64_t e0 =
-      kMode == kRowW
-          ? ((int64_t)blockIdx.x * ((NT / 128) / rpg) + (wave >> 1) / rpg) * kEdgesPerWave
-          : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
+  const RowWave wmap = row_wave(a.C, blockIdx.x, wave, NT / 64);
+  const int half = kMode == kRowW ? wmap.half : 0;
+  const int rpg = kMode == kRowW ? wmap.pairs : 1;
+  const int rsub = kMode == kRowW ? wmap.sub : 0;
+  const int64_t e0 = kMode == kRowW ? wmap.e0
+                                    : ((int64_t)blockIdx.x * (NT / 64) + wave) * kEdgesPerWave;
   const int64_t rows = a.n - e0 < kEdgesPerWave ? a.n - e0 : kEdgesPerWave;
   const auto rx = x_rsrc(a, e0, rows);
   const auto rg = rows_rsrc(gout, e0, a.W1, rows);
